@@ -1,0 +1,133 @@
+/*
+ * pulsar_w4a16.h -- C ABI of the MI355X (gfx950) W4A16 linear-layer library
+ * (libpulsar_w4a16.so).
+ *
+ * Plain pointers and sizes only: every tensor argument is a device pointer
+ * (hipMalloc'd or torch-owned), every size is an element count, every call is
+ * asynchronous on `stream` and returns 0 or a negative PW4_ERR_* status.  No
+ * entry point allocates device memory: scratch space is passed in through
+ * (workspace, workspace_bytes) and sized with the matching *_workspace_size
+ * query, so the GEMMs are safe under HIP graph capture.
+ *
+ * Each entry point replaces one operator of the reference pulsar-core C++ API
+ * (pulsar-core/inc/pulsar/ops.hpp) and keeps its argument meaning and its
+ * precondition checks; the at::Tensor wrappers that keep the reference C++
+ * signatures verbatim live in pulsar_amd/csrc/torch_ops.cpp.
+ */
+#ifndef PULSAR_W4A16_H
+#define PULSAR_W4A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* pw4_stream_t; /* == hipStream_t */
+
+/* status codes */
+#define PW4_OK 0
+#define PW4_ERR_ARG (-1)       /* null pointer, unknown dtype, negative size */
+#define PW4_ERR_SHAPE (-2)     /* inconsistent sizes / group size (reference TORCH_CHECKs) */
+#define PW4_ERR_WORKSPACE (-3) /* workspace missing or smaller than the *_workspace_size query */
+#define PW4_ERR_HIP (-4)       /* a HIP runtime call or kernel launch failed */
+#define PW4_ERR_GIDX (-5)      /* act-order g_idx is not a valid grouping */
+
+/* element types */
+#define PW4_DTYPE_F16 0
+#define PW4_DTYPE_BF16 1
+#define PW4_DTYPE_F32 2
+
+/* Human-readable text for a status code (static storage). */
+const char* pw4_status_string(int status);
+/* Text of the last HIP error seen by this thread inside the library. */
+const char* pw4_last_hip_error(void);
+/* ABI version of this header: bumped on any incompatible change. */
+int pw4_abi_version(void);
+#define PW4_ABI_VERSION 1
+
+/* Number of int32 words of the MARLIN layout for an [N, K] weight:
+ * roundup(N, 64) * roundup(K, 64) / 8.
+ * Mirrors the size rule of repack_w4a16 (pulsar-core/src/kernels/w4a16_marlin.cu:373-375;
+ * pulsar/src/pulsar/core/ops.py:139-155). */
+int64_t pw4_marlin_words(int64_t N, int64_t K);
+
+/* ---------------------------------------------------------------------------
+ * repack_w4a16: compressed-tensors int4 weights -> MARLIN layout.
+ * Replaces pulsar::repack_w4a16_cuda (pulsar-core/inc/pulsar/ops.hpp:181-182;
+ * pulsar-core/src/kernels/w4a16_marlin.cu:354-406).
+ *   weight_packed  int32 [N, K/8], nibble k%8 of word [n, k/8], two's complement
+ *   weight_scale   [N, K/group_size] in scale_dtype (F32, F16 or BF16)
+ *   weight_marlin  out, int32 [pw4_marlin_words(N, K)]  (bit-exact reference layout)
+ *   scale_marlin   out, fp32 [K/group_size, N] = transpose of weight_scale
+ * Preconditions (reference w4a16_marlin.cu:356-371): group_size > 0,
+ * group_size % 16 == 0, K % 8 == 0, K % group_size == 0. */
+int pw4_repack_w4a16(const int32_t* weight_packed, const void* weight_scale, int scale_dtype, int64_t N, int64_t K,
+                     int64_t group_size, int32_t* weight_marlin, float* scale_marlin, pw4_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * gemm_w4a16 / gemm_w4a16_split: y = x @ dequant(W)^T straight from the
+ * compressed-tensors packing.
+ * Replaces pulsar::gemm_w4a16_cuda and pulsar::gemm_w4a16_split_cuda
+ * (pulsar-core/inc/pulsar/ops.hpp:156-173; pulsar-core/src/kernels/w4a16_gemm.cu:317-489).
+ *   x              [M, K] fp16 or bf16 (x_dtype), row-major contiguous
+ *   weight_packed  int32 [N, K/8] as above
+ *   weight_scale   fp32 [N, K/group_size]   (the reference upcasts to fp32 too, w4a16_gemm.cu:352)
+ *   y              out, [M, N] in x_dtype
+ *   num_splits     0: the library picks the K split; >= 1: force exactly that many
+ *                  K slices through the fp32-partials + fixed-order combine path
+ *                  (slices beyond the K extent are empty and add 0), as the
+ *                  reference's gemm_w4a16_split does.
+ * Preconditions (reference w4a16_gemm.cu:324-348): K % 8 == 0, group_size > 0,
+ * group_size % 16 == 0, K % group_size == 0.  M == 0 or N == 0 is a no-op. */
+size_t pw4_gemm_w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group_size, int64_t num_splits);
+int pw4_gemm_w4a16(const void* x, int x_dtype, const int32_t* weight_packed, const float* weight_scale, void* y,
+                   int64_t M, int64_t N, int64_t K, int64_t group_size, int64_t num_splits, void* workspace,
+                   size_t workspace_bytes, pw4_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * gemm_w4a16_marlin: y = x @ dequant(W)^T from the MARLIN layout.
+ * Replaces pulsar::gemm_w4a16_marlin_cuda (pulsar-core/inc/pulsar/ops.hpp:184-189;
+ * pulsar-core/src/kernels/w4a16_marlin.cu:408-551), extended with optional
+ * asymmetric zero points and act-order (neither exists in the reference):
+ *   x              [M, K] fp16 or bf16
+ *   weight_marlin  int32 [pw4_marlin_words(N, K)] from pw4_repack_w4a16 / pw4_repack_gptq
+ *   scales         [K/group_size, N] in scale_dtype (F32 as repack_w4a16 returns, or F16)
+ *   qzeros         NULL (symmetric, zero point 8) or int32 [K/group_size, N/8] GPTQ
+ *                  zero points: nibble n%8 of word [g, n/8], used as stored (w = (u - z) * s)
+ *   perm           NULL or int32 [K]: the act-order permutation from pw4_gidx_to_perm;
+ *                  the kernel computes y = x[:, perm] @ dequant(W_repacked)^T
+ *   num_splits     as for pw4_gemm_w4a16
+ * Preconditions (reference w4a16_marlin.cu:414-442): group_size > 0,
+ * group_size % 16 == 0, K % group_size == 0, K % 8 == 0; N % 8 == 0 when qzeros. */
+size_t pw4_gemm_w4a16_marlin_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm,
+                                            int64_t num_splits);
+int pw4_gemm_w4a16_marlin(const void* x, int x_dtype, const int32_t* weight_marlin, const void* scales,
+                          int scale_dtype, const int32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N,
+                          int64_t K, int64_t group_size, int64_t num_splits, void* workspace,
+                          size_t workspace_bytes, pw4_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * GPTQ ingestion (no counterpart in the reference, which has no zero points
+ * and no act-order; these follow the public GPTQ checkpoint convention).
+ *
+ * pw4_gidx_to_perm: perm = stable argsort(g_idx) for an act-order checkpoint.
+ *   g_idx [K] int32 group id of each input row; every group must hold exactly
+ *   group_size rows.  status_dev is an int32 device word the call zeroes and
+ *   then sets nonzero if g_idx is not such a grouping (read it after the stream
+ *   syncs: nonzero means PW4_ERR_GIDX).
+ * pw4_repack_gptq: qweight int32 [K/8, N] (nibble k%8 of word [k/8, n], unsigned)
+ *   -> MARLIN layout; repacked row j is original row perm[j] (perm may be NULL).
+ *   GPTQ symmetric nibbles and the reference's MARLIN nibbles are the same bytes,
+ *   so for perm == NULL the output equals pw4_repack_w4a16 of the matching
+ *   compressed-tensors tensor. */
+int pw4_gidx_to_perm(const int32_t* g_idx, int64_t K, int64_t group_size, int32_t* perm, int32_t* status_dev,
+                     pw4_stream_t stream);
+int pw4_repack_gptq(const int32_t* qweight, const int32_t* perm, int64_t N, int64_t K, int32_t* weight_marlin,
+                    pw4_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PULSAR_W4A16_H */

@@ -1,0 +1,313 @@
+// C ABI of libpulsar_w4a16.so: argument checks, kernel selection, workspace
+// carving, launches.  Declarations and reference citations: include/pulsar_w4a16.h.
+#include "pulsar_w4a16.h"
+
+#include <algorithm>
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+
+#include "w4a16_common.h"
+#include "w4a16_kernels.h"
+
+using namespace pw4;
+
+namespace {
+
+thread_local char g_last_hip_error[256] = "";
+
+int hip_fail(hipError_t e) {
+    std::snprintf(g_last_hip_error, sizeof(g_last_hip_error), "%s (%d)", hipGetErrorString(e), (int)e);
+    return PW4_ERR_HIP;
+}
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+
+int cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int v = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        g_cu_count[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+// Largest x slice a decode workgroup stages in LDS.
+constexpr size_t kDecodeLdsLimit = 64 * 1024;
+
+struct Plan {
+    bool decode = false;
+    DecodeConfig dc{};
+    int p_splits = 1;        // prefill K splits
+    int p_cps = 0;           // prefill chunks per split
+    bool use_partial = false;
+    int splits = 1;
+    size_t partial_bytes = 0;
+    size_t xperm_bytes = 0;
+    size_t workspace() const { return align_up(partial_bytes) + align_up(xperm_bytes); }
+};
+
+size_t decode_lds(int64_t M, int kps, int G) {
+    const size_t rs = (size_t)kps + 8;
+    const size_t x = (M * rs * 2 + 15) / 16 * 16;
+    const size_t ngl = (size_t)kps / (size_t)G + 2;
+    return x + (size_t)M * ngl * 4;
+}
+
+// layout: LAYOUT_MARLIN or LAYOUT_CT.  num_splits: 0 auto, >= 1 forced.
+Plan make_plan(int layout, int64_t M, int64_t N, int64_t K, int64_t G, bool has_perm, int64_t num_splits) {
+    Plan p;
+    const int cus = cu_count();
+    const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
+    const int64_t ktiles = kext / 32;
+    const bool forced = num_splits >= 1;
+    const bool decode_ok = M <= 64 && (G == 64 || G % 128 == 0);
+    if (decode_ok) {
+        DecodeConfig dc{};
+        dc.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+        dc.ngrp = G == 64 ? 2 : 1;
+        const int64_t cols = layout == LAYOUT_MARLIN ? round_up(N, kMarlinBN) / 64 : ceil_div(N, 64);
+        const int64_t steps = std::max<int64_t>(ceil_div(ktiles * 32, 128), 1);
+        int64_t s;
+        if (forced) {
+            s = num_splits;
+        } else {
+            const int64_t target = 2 * (int64_t)cus;
+            s = std::min<int64_t>(std::max<int64_t>(ceil_div(target, std::max<int64_t>(cols, 1)), 1), steps);
+        }
+        int64_t kps = std::max<int64_t>(round_up(ceil_div(ktiles * 32, s), 128), 128);
+        if (!forced) {
+            while (kps > 128 && decode_lds(M, (int)kps, (int)G) > kDecodeLdsLimit) kps -= 128;
+            s = std::max<int64_t>(ceil_div(ktiles * 32, kps), 1);
+        }
+        dc.k_per_split = (int)kps;
+        dc.splits = (int)s;
+        dc.lds_bytes = decode_lds(M, (int)kps, (int)G);
+        if (dc.lds_bytes <= kDecodeLdsLimit) {
+            p.decode = true;
+            p.dc = dc;
+            p.splits = (int)s;
+            p.use_partial = forced || s > 1;
+        }
+    }
+    if (!p.decode) {
+        const int64_t nchunks = ceil_div(kext, 64);
+        const int64_t base = ceil_div(M, prefill_tile_m()) * ceil_div(N, prefill_tile_n());
+        int64_t s;
+        if (forced) {
+            s = num_splits;
+        } else if (base >= cus || nchunks < 8) {
+            s = 1;
+        } else {
+            s = std::min<int64_t>(ceil_div(cus, std::max<int64_t>(base, 1)), nchunks / 4);
+            s = std::max<int64_t>(s, 1);
+        }
+        int64_t cps = std::max<int64_t>(ceil_div(std::max<int64_t>(nchunks, 1), s), 1);
+        if (!forced) s = std::max<int64_t>(ceil_div(nchunks, cps), 1);
+        p.p_splits = (int)s;
+        p.p_cps = (int)cps;
+        p.splits = (int)s;
+        p.use_partial = forced || s > 1;
+        if (has_perm) p.xperm_bytes = (size_t)M * K * 2;
+    }
+    if (p.use_partial) p.partial_bytes = (size_t)p.splits * M * N * 4;
+    return p;
+}
+
+int check_common(int64_t M, int64_t N, int64_t K, int64_t G, int x_dtype) {
+    if (M < 0 || N < 0 || K < 0) return PW4_ERR_ARG;
+    if (x_dtype != PW4_DTYPE_F16 && x_dtype != PW4_DTYPE_BF16) return PW4_ERR_ARG;
+    if (G <= 0 || G % 16 != 0) return PW4_ERR_SHAPE;
+    if (K % 8 != 0 || K % G != 0) return PW4_ERR_SHAPE;
+    if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return PW4_ERR_SHAPE;
+    return PW4_OK;
+}
+
+int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const void* scales, int stype,
+             const uint32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N, int64_t K, int64_t G,
+             int64_t num_splits, void* workspace, size_t ws_bytes, hipStream_t stream) {
+    const Plan p = make_plan(layout, M, N, K, G, perm != nullptr, num_splits);
+    if (p.workspace() > 0 && (workspace == nullptr || ws_bytes < p.workspace())) return PW4_ERR_WORKSPACE;
+    char* ws = reinterpret_cast<char*>(workspace);
+    float* partial = p.partial_bytes ? reinterpret_cast<float*>(ws) : nullptr;
+    uint16_t* xperm = p.xperm_bytes ? reinterpret_cast<uint16_t*>(ws + align_up(p.partial_bytes)) : nullptr;
+    const int xt = x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16;
+    const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
+    hipError_t e;
+    if (p.decode) {
+        DecodeArgs a{};
+        a.x = reinterpret_cast<const uint16_t*>(x);
+        a.w = w;
+        a.scales = scales;
+        a.qzeros = qzeros;
+        a.perm = perm;
+        a.y = reinterpret_cast<uint16_t*>(y);
+        a.partial = p.use_partial ? partial : nullptr;
+        a.M = (int)M;
+        a.N = (int)N;
+        a.K = (int)K;
+        a.G = (int)G;
+        a.Kg = (int)(K / G);
+        a.ktiles = (int)(kext / 32);
+        a.nchunks = (int)(round_up(K, kMarlinBK) / kMarlinBK);
+        a.k_per_split = p.dc.k_per_split;
+        a.rowstride = p.dc.k_per_split + 8;
+        a.splits = p.dc.splits;
+        const int grid_x = (int)(layout == LAYOUT_MARLIN ? round_up(N, kMarlinBN) / 64 : ceil_div(N, 64));
+        e = launch_decode(layout, xt, stype, qzeros != nullptr, p.dc, a, grid_x, stream);
+        if (e != hipSuccess) return hip_fail(e);
+    } else {
+        const uint16_t* xin = reinterpret_cast<const uint16_t*>(x);
+        if (perm) {
+            e = launch_gather_x(xin, perm, xperm, (int)M, (int)K, stream);
+            if (e != hipSuccess) return hip_fail(e);
+            xin = xperm;
+        }
+        PrefillArgs a{};
+        a.x = xin;
+        a.w = w;
+        a.scales = scales;
+        a.qzeros = qzeros;
+        a.y = reinterpret_cast<uint16_t*>(y);
+        a.partial = p.use_partial ? partial : nullptr;
+        a.M = (int)M;
+        a.N = (int)N;
+        a.K = (int)K;
+        a.G = (int)G;
+        a.Kg = (int)(K / G);
+        a.ktiles = (int)(kext / 32);
+        a.nchunks = (int)ceil_div(kext, 64);
+        a.chunks_per_split = p.p_cps;
+        a.splits = p.p_splits;
+        e = launch_prefill(layout, xt, stype, qzeros != nullptr, a, stream);
+        if (e != hipSuccess) return hip_fail(e);
+    }
+    if (p.use_partial) {
+        e = launch_combine(partial, reinterpret_cast<uint16_t*>(y), M * N, p.splits, xt, stream);
+        if (e != hipSuccess) return hip_fail(e);
+    }
+    return PW4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pw4_status_string(int status) {
+    switch (status) {
+        case PW4_OK: return "ok";
+        case PW4_ERR_ARG: return "invalid argument (null pointer, dtype or negative size)";
+        case PW4_ERR_SHAPE: return "inconsistent shape or group size";
+        case PW4_ERR_WORKSPACE: return "workspace missing or too small";
+        case PW4_ERR_HIP: return "HIP runtime error";
+        case PW4_ERR_GIDX: return "g_idx is not a grouping of exactly group_size rows per group";
+        default: return "unknown status";
+    }
+}
+
+const char* pw4_last_hip_error(void) { return g_last_hip_error; }
+
+int pw4_abi_version(void) { return PW4_ABI_VERSION; }
+
+int64_t pw4_marlin_words(int64_t N, int64_t K) {
+    if (N < 0 || K < 0) return 0;
+    return round_up(N, kMarlinBN) * round_up(K, kMarlinBK) / 8;
+}
+
+int pw4_repack_w4a16(const int32_t* weight_packed, const void* weight_scale, int scale_dtype, int64_t N, int64_t K,
+                     int64_t group_size, int32_t* weight_marlin, float* scale_marlin, pw4_stream_t stream) {
+    if (N < 0 || K < 0) return PW4_ERR_ARG;
+    if (group_size <= 0 || group_size % 16 != 0) return PW4_ERR_SHAPE;
+    if (K % 8 != 0 || K % group_size != 0) return PW4_ERR_SHAPE;
+    if (N > INT32_MAX || K > INT32_MAX) return PW4_ERR_SHAPE;
+    int st;
+    switch (scale_dtype) {
+        case PW4_DTYPE_F32: st = 0; break;
+        case PW4_DTYPE_F16: st = 1; break;
+        case PW4_DTYPE_BF16: st = 2; break;
+        default: return PW4_ERR_ARG;
+    }
+    if (N > 0 && K > 0 && (!weight_packed || !weight_marlin)) return PW4_ERR_ARG;
+    if (N > 0 && K > 0 && (!weight_scale || !scale_marlin)) return PW4_ERR_ARG;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    hipError_t e = launch_repack_ct(reinterpret_cast<const uint32_t*>(weight_packed),
+                                    reinterpret_cast<uint32_t*>(weight_marlin), (int)N, (int)K, s);
+    if (e != hipSuccess) return hip_fail(e);
+    e = launch_scale_transpose(weight_scale, st, scale_marlin, (int)N, (int)(K / group_size), s);
+    if (e != hipSuccess) return hip_fail(e);
+    return PW4_OK;
+}
+
+size_t pw4_gemm_w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group_size, int64_t num_splits) {
+    if (check_common(M, N, K, group_size, PW4_DTYPE_F16) != PW4_OK || M == 0 || N == 0) return 0;
+    return make_plan(LAYOUT_CT, M, N, K, group_size, false, num_splits).workspace();
+}
+
+int pw4_gemm_w4a16(const void* x, int x_dtype, const int32_t* weight_packed, const float* weight_scale, void* y,
+                   int64_t M, int64_t N, int64_t K, int64_t group_size, int64_t num_splits, void* workspace,
+                   size_t workspace_bytes, pw4_stream_t stream) {
+    int rc = check_common(M, N, K, group_size, x_dtype);
+    if (rc != PW4_OK) return rc;
+    if (num_splits < 0) return PW4_ERR_ARG;
+    if (M == 0 || N == 0) return PW4_OK;
+    if (!x || !weight_packed || !weight_scale || !y) return PW4_ERR_ARG;
+    return run_gemm(LAYOUT_CT, x, x_dtype, reinterpret_cast<const uint32_t*>(weight_packed), weight_scale, S_F32,
+                    nullptr, nullptr, y, M, N, K, group_size, num_splits, workspace, workspace_bytes,
+                    reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t pw4_gemm_w4a16_marlin_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm,
+                                            int64_t num_splits) {
+    if (check_common(M, N, K, group_size, PW4_DTYPE_F16) != PW4_OK || M == 0 || N == 0) return 0;
+    return make_plan(LAYOUT_MARLIN, M, N, K, group_size, has_perm != 0, num_splits).workspace();
+}
+
+int pw4_gemm_w4a16_marlin(const void* x, int x_dtype, const int32_t* weight_marlin, const void* scales,
+                          int scale_dtype, const int32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N,
+                          int64_t K, int64_t group_size, int64_t num_splits, void* workspace,
+                          size_t workspace_bytes, pw4_stream_t stream) {
+    int rc = check_common(M, N, K, group_size, x_dtype);
+    if (rc != PW4_OK) return rc;
+    if (num_splits < 0) return PW4_ERR_ARG;
+    if (scale_dtype != PW4_DTYPE_F32 && scale_dtype != PW4_DTYPE_F16) return PW4_ERR_ARG;
+    if (qzeros && N % 8 != 0) return PW4_ERR_SHAPE;
+    if (M == 0 || N == 0) return PW4_OK;
+    if (!x || !weight_marlin || !scales || !y) return PW4_ERR_ARG;
+    return run_gemm(LAYOUT_MARLIN, x, x_dtype, reinterpret_cast<const uint32_t*>(weight_marlin), scales,
+                    scale_dtype == PW4_DTYPE_F32 ? S_F32 : S_F16, reinterpret_cast<const uint32_t*>(qzeros), perm, y,
+                    M, N, K, group_size, num_splits, workspace, workspace_bytes,
+                    reinterpret_cast<hipStream_t>(stream));
+}
+
+int pw4_gidx_to_perm(const int32_t* g_idx, int64_t K, int64_t group_size, int32_t* perm, int32_t* status_dev,
+                     pw4_stream_t stream) {
+    if (K < 0 || K > INT32_MAX) return PW4_ERR_ARG;
+    if (group_size <= 0 || K % group_size != 0) return PW4_ERR_SHAPE;
+    if (!status_dev || (K > 0 && (!g_idx || !perm))) return PW4_ERR_ARG;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    hipError_t e = hipMemsetAsync(status_dev, 0, sizeof(int32_t), s);
+    if (e != hipSuccess) return hip_fail(e);
+    e = launch_gidx_perm(g_idx, perm, status_dev, (int)K, (int)group_size, s);
+    if (e != hipSuccess) return hip_fail(e);
+    return PW4_OK;
+}
+
+int pw4_repack_gptq(const int32_t* qweight, const int32_t* perm, int64_t N, int64_t K, int32_t* weight_marlin,
+                    pw4_stream_t stream) {
+    if (N < 0 || K < 0 || N > INT32_MAX || K > INT32_MAX) return PW4_ERR_ARG;
+    if (K % 8 != 0) return PW4_ERR_SHAPE;
+    if (N > 0 && K > 0 && (!qweight || !weight_marlin)) return PW4_ERR_ARG;
+    hipError_t e = launch_repack_gptq(reinterpret_cast<const uint32_t*>(qweight), perm,
+                                      reinterpret_cast<uint32_t*>(weight_marlin), (int)N, (int)K,
+                                      reinterpret_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e);
+    return PW4_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,189 @@
+// One-time weight re-layout kernels.
+//
+// Both repacks emit the reference MARLIN word layout (pulsar-core/src/kernels/
+// w4a16_marlin.cu:27-54): for column n and 32-wide K tile t the four words
+// tg = 0..3 are 16 contiguous bytes at
+//     ((n/64 * nchunks + t/2) * 512 + (t%2) * 256 + (n%64) * 4) words,
+// and nibble p of word tg holds K offset (p%4)*8 + 2tg + p/4 of the tile, stored
+// unsigned (signed + 8), with 8 in padding.  A thread builds those 16 bytes
+// for one (n, t): if b_j is byte tg of source word j (K 8j..8j+7 of the tile),
+// word tg = sum_j (b_j & 0xf) << 4j | (b_j >> 4) << (16 + 4j).
+//
+// The reference builds each word with eight scattered nibble reads
+// (w4a16_marlin.cu:139-174); here each thread reads the tile's four source
+// words once and writes 16 contiguous bytes, so for a fixed tile the threads
+// of a 64-column block write one contiguous 1 KB run.
+#include "w4a16_common.h"
+#include "w4a16_kernels.h"
+
+namespace pw4 {
+namespace {
+
+__device__ __forceinline__ u32x4 transpose_tile_bytes(const uint32_t src[4]) {
+    u32x4 out;
+#pragma unroll
+    for (int tg = 0; tg < 4; ++tg) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t b = (src[j] >> (8 * tg)) & 0xffu;
+            w |= (b & 0xfu) << (4 * j);
+            w |= (b >> 4) << (16 + 4 * j);
+        }
+        out[tg] = w;
+    }
+    return out;
+}
+
+__device__ __forceinline__ int64_t marlin_offset(int n, int t, int nchunks) {
+    return ((int64_t)(n >> 6) * nchunks + (t >> 1)) * kChunkWords + (t & 1) * 256 + (n & 63) * 4;
+}
+
+// compressed-tensors [N, K/8] (signed) -> MARLIN.  grid: (Npad/64, Kpad/32), block 64.
+__global__ __launch_bounds__(64) void repack_ct_kernel(const uint32_t* __restrict__ packed, uint32_t* __restrict__ wm,
+                                                       int N, int K, int nchunks) {
+    const int n = blockIdx.x * 64 + threadIdx.x;
+    const int t = blockIdx.y;
+    uint32_t src[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = t * 32 + j * 8;  // K % 8 == 0: a source word is all-in or all-out
+        // signed nibble s -> u = s ^ 8; out-of-range -> u = 8 (dequantizes to 0)
+        src[j] = (n < N && k < K) ? (packed[(int64_t)n * (K / 8) + k / 8] ^ 0x88888888u) : 0x88888888u;
+    }
+    *reinterpret_cast<u32x4*>(wm + marlin_offset(n, t, nchunks)) = transpose_tile_bytes(src);
+}
+
+// GPTQ qweight [K/8, N] (unsigned) -> MARLIN, rows gathered through perm when
+// given (repacked row j = original row perm[j]).  grid: (Npad/64, Kpad/32).
+__global__ __launch_bounds__(64) void repack_gptq_kernel(const uint32_t* __restrict__ qweight,
+                                                         const int32_t* __restrict__ perm,
+                                                         uint32_t* __restrict__ wm, int N, int K, int nchunks) {
+    const int n = blockIdx.x * 64 + threadIdx.x;
+    const int t = blockIdx.y;
+    uint32_t src[4];
+    if (perm == nullptr) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = t * 32 + j * 8;
+            src[j] = (n < N && k < K) ? qweight[(int64_t)(k / 8) * N + n] : 0x88888888u;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int k = t * 32 + j * 8 + e;
+                uint32_t nib = 8u;
+                if (n < N && k < K) {
+                    const int sk = min(max(perm[k], 0), K - 1);  // clamped: a bad perm cannot fault
+                    nib = (qweight[(int64_t)(sk >> 3) * N + n] >> (4 * (sk & 7))) & 0xfu;
+                }
+                w |= nib << (4 * e);
+            }
+            src[j] = w;
+        }
+    }
+    *reinterpret_cast<u32x4*>(wm + marlin_offset(n, t, nchunks)) = transpose_tile_bytes(src);
+}
+
+// scale_marlin[g, n] = (float) weight_scale[n, g]   (w4a16_marlin.cu:177-185)
+template <typename T>
+__global__ __launch_bounds__(256) void scale_transpose_kernel(const T* __restrict__ ws, float* __restrict__ sm, int N,
+                                                              int Kg) {
+    __shared__ float tile[32][33];
+    const int g0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int r = ty; r < 32; r += 8) {
+        const int n = n0 + r, g = g0 + tx;
+        tile[r][tx] = (n < N && g < Kg) ? load_scale(ws + (int64_t)n * Kg + g) : 0.f;
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        const int g = g0 + r, n = n0 + tx;
+        if (g < Kg && n < N) sm[(int64_t)g * N + n] = tile[tx][r];
+    }
+}
+
+// perm = stable argsort(g_idx) for an act-order checkpoint: one workgroup per
+// group collects, in ascending k, the rows that belong to it.  status bit 0:
+// some group does not hold exactly G rows; bit 1: a group id out of range.
+__global__ __launch_bounds__(256) void gidx_perm_kernel(const int32_t* __restrict__ g_idx, int32_t* __restrict__ perm,
+                                                        int32_t* __restrict__ status, int K, int G) {
+    __shared__ int wave_cnt[4];
+    const int g = blockIdx.x;
+    const int Kg = K / G;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    int base_count = 0;
+    for (int k0 = 0; k0 < K; k0 += 256) {
+        const int k = k0 + tid;
+        const int gv = k < K ? g_idx[k] : -1;
+        if (g == 0 && k < K && (gv < 0 || gv >= Kg)) atomicOr(status, 2);
+        const bool mine = k < K && gv == g;
+        const uint64_t mask = __ballot(mine);
+        const int before_lane = __popcll(mask & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_cnt[wave] = __popcll(mask);
+        __syncthreads();
+        int before_wave = 0, total = 0;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            before_wave += w < wave ? wave_cnt[w] : 0;
+            total += wave_cnt[w];
+        }
+        const int pos = base_count + before_wave + before_lane;
+        if (mine && pos < G) perm[(int64_t)g * G + pos] = k;
+        base_count += total;
+        __syncthreads();
+    }
+    if (tid == 0 && base_count != G) atomicOr(status, 1);
+}
+
+}  // namespace
+
+hipError_t launch_repack_ct(const uint32_t* packed, uint32_t* wm, int N, int K, hipStream_t stream) {
+    const int npad = (int)round_up(N, kMarlinBN), kpad = (int)round_up(K, kMarlinBK);
+    if (npad == 0 || kpad == 0) return hipSuccess;
+    hipLaunchKernelGGL(repack_ct_kernel, dim3(npad / 64, kpad / 32), dim3(64), 0, stream, packed, wm, N, K,
+                       kpad / kMarlinBK);
+    return hipGetLastError();
+}
+
+hipError_t launch_repack_gptq(const uint32_t* qweight, const int32_t* perm, uint32_t* wm, int N, int K,
+                              hipStream_t stream) {
+    const int npad = (int)round_up(N, kMarlinBN), kpad = (int)round_up(K, kMarlinBK);
+    if (npad == 0 || kpad == 0) return hipSuccess;
+    hipLaunchKernelGGL(repack_gptq_kernel, dim3(npad / 64, kpad / 32), dim3(64), 0, stream, qweight, perm, wm, N, K,
+                       kpad / kMarlinBK);
+    return hipGetLastError();
+}
+
+hipError_t launch_scale_transpose(const void* ws, int stype_in, float* sm, int N, int Kg, hipStream_t stream) {
+    if (N == 0 || Kg == 0) return hipSuccess;
+    const dim3 grid((unsigned)ceil_div(Kg, 32), (unsigned)ceil_div(N, 32));
+    switch (stype_in) {
+        case 0:
+            hipLaunchKernelGGL(scale_transpose_kernel<float>, grid, dim3(256), 0, stream,
+                               reinterpret_cast<const float*>(ws), sm, N, Kg);
+            break;
+        case 1:
+            hipLaunchKernelGGL(scale_transpose_kernel<_Float16>, grid, dim3(256), 0, stream,
+                               reinterpret_cast<const _Float16*>(ws), sm, N, Kg);
+            break;
+        case 2:
+            hipLaunchKernelGGL(scale_transpose_kernel<__bf16>, grid, dim3(256), 0, stream,
+                               reinterpret_cast<const __bf16*>(ws), sm, N, Kg);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gidx_perm(const int32_t* g_idx, int32_t* perm, int32_t* status, int K, int G, hipStream_t stream) {
+    if (K == 0) return hipSuccess;
+    hipLaunchKernelGGL(gidx_perm_kernel, dim3(K / G), dim3(256), 0, stream, g_idx, perm, status, K, G);
+    return hipGetLastError();
+}
+
+}  // namespace pw4
