@@ -6,8 +6,8 @@
 // reference TORCH_CHECKs (w4a16_gemm.cu:324-348, w4a16_marlin.cu:356-371,414-442).
 #include "pulsar_w4a16_ops.hpp"
 
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
 
 #include "pulsar_w4a16.h"
@@ -19,8 +19,12 @@ constexpr int64_t kMarlinBN = 64, kMarlinBK = 64;
 
 int64_t roundup(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+// ROCm PyTorch keeps HIP devices under the CUDA device type ("masquerading"),
+// so the guard and the current-stream query are the masquerading variants.
+using DeviceGuard = c10::hip::HIPGuardMasqueradingAsCUDA;
+
 pw4_stream_t current_stream() {
-    return reinterpret_cast<pw4_stream_t>(c10::hip::getCurrentHIPStream().stream());
+    return reinterpret_cast<pw4_stream_t>(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
 }
 
 void check_status(int rc, const char* op) {
@@ -54,7 +58,7 @@ at::Tensor gemm_w4a16_run(const at::Tensor& x, const at::Tensor& weight_packed, 
     TORCH_CHECK(weight_scale.size(0) == N && weight_scale.size(1) == K / group_size,
                 "gemm_w4a16: weight_scale must be [N, K/group_size]");
 
-    c10::hip::HIPGuard guard(x.device());
+    DeviceGuard guard(x.device());
     auto wp = weight_packed.contiguous();
     auto ws = weight_scale.to(at::kFloat).contiguous();
     auto y = at::empty({M, N}, x.options());
@@ -105,7 +109,7 @@ at::Tensor marlin_run(const at::Tensor& x, const at::Tensor& weight_marlin, cons
         pc = perm->contiguous();
         pp = pc.data_ptr<int32_t>();
     }
-    c10::hip::HIPGuard guard(x.device());
+    DeviceGuard guard(x.device());
     auto wm = weight_marlin.contiguous();
     auto sm = scales.contiguous();
     auto y = at::empty({M, N}, x.options());
@@ -148,7 +152,7 @@ std::tuple<at::Tensor, at::Tensor> repack_w4a16_cuda(const at::Tensor& weight_pa
     const auto st = weight_scale.scalar_type();
     TORCH_CHECK(st == at::kFloat || st == at::kHalf || st == at::kBFloat16,
                 "repack_w4a16: weight_scale must be fp32, fp16 or bf16");
-    c10::hip::HIPGuard guard(weight_packed.device());
+    DeviceGuard guard(weight_packed.device());
     auto wp = weight_packed.contiguous();
     auto ws = weight_scale.contiguous();
     auto weight_marlin = at::empty({pw4_marlin_words(N, K)}, wp.options());
@@ -183,7 +187,7 @@ std::tuple<at::Tensor, at::Tensor> repack_w4a16_gptq_cuda(const at::Tensor& qwei
                 "repack_w4a16_gptq: group_size must be a positive multiple of 16");
     const int64_t K = qweight.size(0) * 8, N = qweight.size(1);
     TORCH_CHECK(K % group_size == 0, "repack_w4a16_gptq: K must be a multiple of group_size");
-    c10::hip::HIPGuard guard(qweight.device());
+    DeviceGuard guard(qweight.device());
     auto qw = qweight.contiguous();
     auto weight_marlin = at::empty({pw4_marlin_words(N, K)}, qw.options());
     at::Tensor perm = at::empty({0}, qw.options());
