@@ -1,26 +1,37 @@
 """W4A16 benchmark on one MI355X.
 
-Workload of the headline line: the Llama-3-8B decode
-sweep, M in {1, 4, 8, 16} x {qkv 4096x6144, o 4096x4096, gate_up 4096x28672,
-down 14336x4096}, symmetric int4, group 128, fp16 activations.  One "step" is
-one pass over the 16 GEMMs (repacked MARLIN weights, inputs resident in HBM).
+Headline workload: the Llama-3-8B decode sweep,
+M in {1, 4, 8, 16} x {qkv 4096x6144, o 4096x4096, gate_up 4096x28672,
+down 14336x4096}, symmetric int4, group 128, fp16 scales, fp16 activations.
+One "step" is one pass over the 16 (layer, M) GEMMs, each launched R times
+on distinct weight copies.  Inputs are resident in HBM before timing starts.
 
-MALL: MI355X's 256 MB Infinity Cache would hold any single decode shape, so
-every layer has R distinct weight copies used round-robin; between two uses of
-the same copy the sweep streams R x 109 MB >= 512 MB of other weights.
+Timing.  Each (layer, M) shape is captured once into a HIP graph of R
+launches (weight copies rotated inside the graph), so launches run
+back-to-back on the GPU without host launch gaps.  The timed region replays
+the 16 shape graphs per step, each bracketed by HIP events recorded on the
+replay stream.
+  value    = algorithmic bytes of every timed launch / wall time of the
+             timed region (GB/s, whole job).
+  roofline = the decode kernel: algorithmic bytes / summed event time of the
+             shape graphs (per-launch mean), vs 8 TB/s HBM3E.
+Algorithmic bytes per GEMM: N*K/2 (int4) + N*(K/G)*2 (fp16 scales) +
+M*K*2 (x) + M*N*2 (y).
 
-value     = algorithmic bytes of all timed GEMMs / wall time of the timed region
-            (GB/s, whole job).  Algorithmic bytes per GEMM:
-            N*K/2 (int4) + N*(K/G)*2 (fp16 scales) + M*K*2 + M*N*2.
-roofline  = the decode kernel: bytes per launch / mean launch duration from HIP
-            events recorded around each launch on the op's stream, vs 8 TB/s.
-prefill   = the M=4096 prefill sweep (BASELINE configs[2] at its largest M),
-            TFLOP/s = 2*M*N*K / mean launch time, vs 2516.6 TFLOP/s.
-cpu_baseline = the reference CPU path (dequantize to fp32, fp32 GEMM: the
-            reference test oracle restated in oracle/) on this host's cores,
-            over one pass of the same decode sweep.
+MALL.  MI355X's 256 MB Infinity Cache would hold any one decode layer, so
+each layer has C distinct weight copies; with R = 4 and C = 8 a copy is
+reused only after ~850 MB of other weights have streamed through.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-prefill] [--no-cpu]
+Also reported:
+  reference_api = the same sweep through the reference's API
+                  (gemm_w4a16_marlin with fp32 scale_marlin from repack_w4a16);
+  prefill       = M = 4096 over the same layers, TFLOP/s
+                  = 2*M*N*K / mean launch time, vs 2516.6 TFLOP/s fp16 MFMA;
+  cpu_baseline  = the reference CPU path (dequantize to fp32, fp32 GEMM --
+                  the reference test oracle restated in oracle/) on this
+                  host's cores over a bounded sample of the sweep.
+
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-prefill] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -41,6 +52,8 @@ LLAMA8B = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 28672), ("d
 DECODE_M = [1, 4, 8, 16]
 PREFILL_M = 4096
 G = 128
+COPIES = 8
+REPS = 4
 
 
 def decode_bytes(m: int, k: int, n: int, g: int = G) -> int:
@@ -48,6 +61,7 @@ def decode_bytes(m: int, k: int, n: int, g: int = G) -> int:
 
 
 def make_weights(k: int, n: int, copies: int, dev):
+    """`copies` independent random int4 weights: (MARLIN words, fp32 [K/G,N] scales, fp16 [K/G,N] scales)."""
     import torch
 
     import pulsar_amd
@@ -57,40 +71,40 @@ def make_weights(k: int, n: int, copies: int, dev):
         packed = torch.randint(-(2 ** 31), 2 ** 31, (n, k // 8), dtype=torch.int32, device=dev)
         scale = (torch.randn(n, k // G, device=dev) * 0.02).abs_().add_(1e-3).half()
         wm, sm = pulsar_amd.ops.repack_w4a16(packed, scale, G)
-        out.append((wm, sm))
+        out.append((wm, sm, sm.half()))
         del packed
     return out
 
 
-def cpu_baseline(time_budget_s: float = 20.0) -> dict:
-    """The reference CPU path timed on this host over one pass of the decode sweep."""
+def cpu_baseline(time_budget_s: float = 12.0) -> dict:
+    """The reference CPU path timed on this host over passes of the decode sweep."""
     import numpy as np
 
     from oracle import oracle as O
 
-    tot_bytes, tot_time, shapes = 0, 0.0, 0
-    t_start = time.perf_counter()
     rng = np.random.default_rng(0)
-    for m in DECODE_M:
-        for _, k, n in LLAMA8B:
-            if time.perf_counter() - t_start > time_budget_s:
-                break
-            packed = rng.integers(-(2 ** 31), 2 ** 31, size=(n, k // 8), dtype=np.int64).astype(np.int32)
-            scale = (np.abs(rng.standard_normal((n, k // G))) * 0.02 + 1e-3).astype(np.float32)
-            x = rng.standard_normal((m, k)).astype(np.float32)
-            wbuf = np.empty((n, k), dtype=np.float32)
-            t0 = time.perf_counter()
-            O.w4a16_ct_forward(x, packed, scale, G, wbuf)
-            tot_time += time.perf_counter() - t0
-            tot_bytes += decode_bytes(m, k, n)
-            shapes += 1
+    data = []
+    for _, k, n in LLAMA8B:
+        packed = rng.integers(-(2 ** 31), 2 ** 31, size=(n, k // 8), dtype=np.int64).astype(np.int32)
+        scale = (np.abs(rng.standard_normal((n, k // G))) * 0.02 + 1e-3).astype(np.float32)
+        data.append((k, n, packed, scale, np.empty((n, k), dtype=np.float32)))
+    xs = {(m, k): rng.standard_normal((m, k)).astype(np.float32) for m in DECODE_M for _, k, _ in LLAMA8B}
+    tot_bytes, tot_time, gemms = 0, 0.0, 0
+    while tot_time < time_budget_s:
+        for m in DECODE_M:
+            for k, n, packed, scale, wbuf in data:
+                t0 = time.perf_counter()
+                O.w4a16_ct_forward(xs[(m, k)], packed, scale, G, wbuf)
+                tot_time += time.perf_counter() - t0
+                tot_bytes += decode_bytes(m, k, n)
+                gemms += 1
     return {
         "value": round(tot_bytes / tot_time / 1e9, 3),
         "unit": "GB/s",
         "cores": O.num_threads(),
         "kind": "port",
-        "sample": f"one pass over {shapes} of the 16 decode-sweep GEMMs (dequantize to fp32 + OpenMP fp32 GEMM, "
-                  f"oracle/w4a16_oracle.c), {tot_time:.1f} s of CPU work",
+        "sample": f"{gemms // 16} passes over the 16 decode-sweep GEMMs ({gemms} GEMMs, {tot_time:.1f} s of CPU "
+                  "work): dequantize to fp32 + OpenMP fp32 GEMM, oracle/w4a16_oracle.c",
     }
 
 
@@ -104,14 +118,56 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def build_graphs(torch, shapes, weights, xs, fn, stream):
+    """One graph per (layer, M): REPS launches on rotating weight copies."""
+    graphs = []
+    for mi, (m, name, k, n) in enumerate(shapes):
+        copies = weights[name]
+        first = (DECODE_M.index(m) % 2) * REPS  # M values alternate between copy halves
+        idx = [(first + r) % len(copies) for r in range(REPS)]
+        with torch.cuda.stream(stream):
+            for i in idx:  # eager warm-up on the capture stream (workspace, code objects)
+                fn(xs[(m, k)], copies[i])
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            outs = [fn(xs[(m, k)], copies[i]) for i in idx]
+        graphs.append((g, outs))
+    return graphs
+
+
+def time_graphs(torch, graphs, shapes, steps, warmup, stream):
+    for _ in range(warmup):
+        for g, _ in graphs:
+            g.replay()
+    torch.cuda.synchronize()
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in graphs]
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        for s in range(steps):
+            for i, (g, _) in enumerate(graphs):
+                evs[s][i][0].record(stream)
+                g.replay()
+                evs[s][i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_shape = []
+    for i in range(len(graphs)):
+        ms = sum(evs[s][i][0].elapsed_time(evs[s][i][1]) for s in range(steps)) / steps / REPS
+        per_shape.append(ms)
+    return wall, per_shape
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--copies", type=int, default=6)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-reference-api", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=10)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -125,45 +181,38 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
-    weights = {name: make_weights(k, n, args.copies, dev) for name, k, n in LLAMA8B}
+    weights = {name: make_weights(k, n, COPIES, dev) for name, k, n in LLAMA8B}
     xs = {(m, k): torch.randn(m, k, device=dev).half() for m in DECODE_M for _, k, _ in LLAMA8B}
-    plan = [(m, name, k, n) for m in DECODE_M for name, k, n in LLAMA8B]
-    counter = [0]
+    shapes = [(m, name, k, n) for m in DECODE_M for name, k, n in LLAMA8B]
+    stream = torch.cuda.Stream(device=dev)
 
-    def run_gemm(m, name, k, n):
-        wm, sm = weights[name][counter[0] % args.copies]
-        counter[0] += 1
-        return pulsar_amd.ops.gemm_w4a16_marlin(xs[(m, k)], wm, sm, G)
+    def gemm_fp16_scales(x, w):
+        return pulsar_amd.ops.gemm_w4a16_gptq(x, w[0], w[2], None, None, G)
 
-    for _ in range(args.warmup):
-        for item in plan:
-            run_gemm(*item)
-    torch.cuda.synchronize()
+    def gemm_reference_api(x, w):
+        return pulsar_amd.ops.gemm_w4a16_marlin(x, w[0], w[1], G)
 
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in plan]
-           for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s in range(args.steps):
-        for i, item in enumerate(plan):
-            evs[s][i][0].record()
-            run_gemm(*item)
-            evs[s][i][1].record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-
+    graphs = build_graphs(torch, shapes, weights, xs, gemm_fp16_scales, stream)
+    wall, per_ms = time_graphs(torch, graphs, shapes, args.steps, args.warmup, stream)
+    launches = args.steps * REPS
+    tot_bytes = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) * launches
+    tot_event_s = sum(per_ms) * 1e-3 * launches
     per_gemm = {}
-    tot_bytes = 0
-    tot_launch_ms = 0.0
-    for i, (m, name, k, n) in enumerate(plan):
-        ms = sum(evs[s][i][0].elapsed_time(evs[s][i][1]) for s in range(args.steps)) / args.steps
-        b = decode_bytes(m, k, n)
-        tot_bytes += b * args.steps
-        tot_launch_ms += ms * args.steps
-        per_gemm[f"{name}_m{m}"] = {"us": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
-                                    "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+    for (m, name, k, n), ms in zip(shapes, per_ms):
+        gbs = decode_bytes(m, k, n) / (ms * 1e-3) / 1e9
+        per_gemm[f"{name}_m{m}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
     value = tot_bytes / wall / 1e9
-    achieved = tot_bytes / (tot_launch_ms * 1e-3) / 1e9
+    achieved = tot_bytes / tot_event_s / 1e9
+    del graphs
+
+    ref_api = None
+    if not args.no_reference_api:
+        g2 = build_graphs(torch, shapes, weights, xs, gemm_reference_api, stream)
+        wall2, per2 = time_graphs(torch, g2, shapes, args.steps, args.warmup, stream)
+        ref_api = {"value": round(tot_bytes / wall2 / 1e9, 2), "unit": "GB/s",
+                   "per_gemm_us": {f"{name}_m{m}": round(ms * 1e3, 2) for (m, name, _, _), ms in zip(shapes, per2)}}
+        del g2
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "decode_traffic.json")
@@ -178,14 +227,15 @@ def main() -> int:
         prefill = {}
         for name, k, n in LLAMA8B:
             x = torch.randn(PREFILL_M, k, device=dev).half()
-            wm, sm = weights[name][0]
+            w = weights[name][0]
             for _ in range(2):
-                pulsar_amd.ops.gemm_w4a16_marlin(x, wm, sm, G)
+                gemm_fp16_scales(x, w)
             ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                   for _ in range(args.prefill_reps)]
-            for a, b in ev:
+            for i, (a, b) in enumerate(ev):
+                w = weights[name][i % COPIES]
                 a.record()
-                pulsar_amd.ops.gemm_w4a16_marlin(x, wm, sm, G)
+                gemm_fp16_scales(x, w)
                 b.record()
             torch.cuda.synchronize()
             ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
@@ -212,10 +262,13 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": "llama3-8b W4A16 decode sweep: M in {1,4,8,16} x {qkv 4096x6144, o 4096x4096, "
-                        "gate_up 4096x28672, down 14336x4096}, symmetric int4 G=128 MARLIN layout, fp16 x",
-            "weight_copies": args.copies,
-            "mall_safe": f"round-robin over {args.copies} weight copies per layer",
-            "gemms_per_step": len(plan),
+                        "gate_up 4096x28672, down 14336x4096}, symmetric int4 G=128 fp16 scales, MARLIN "
+                        "layout, fp16 x",
+            "launches_per_gemm_per_step": REPS,
+            "weight_copies": COPIES,
+            "mall_safe": f"each layer rotates over {COPIES} weight copies; a copy is reused after ~850 MB "
+                         "of other weights",
+            "timing": "per-shape HIP graphs of back-to-back launches, HIP events on the replay stream",
         },
         "roofline": {
             "bound": "hbm",
@@ -226,6 +279,7 @@ def main() -> int:
             "traffic": traffic,
         },
         "decode": per_gemm,
+        "reference_api": ref_api,
         "prefill": prefill,
         "cpu_baseline": cpu,
     }

@@ -9,6 +9,13 @@
  * (workspace, workspace_bytes) and sized with the matching *_workspace_size
  * query, so the GEMMs are safe under HIP graph capture.
  *
+ * Workspace contract.  A non-empty workspace begins with a counter region of
+ * PW4_COUNTER_REGION_BYTES that must be zero when the workspace is first
+ * used (clear it once after allocating); every GEMM call leaves it zero when
+ * it completes, so the workspace can be reused by later calls without
+ * clearing.  Calls that share a workspace must be ordered (one stream, or
+ * explicit synchronisation); concurrent calls need distinct workspaces.
+ *
  * Each entry point replaces one operator of the reference pulsar-core C++ API
  * (pulsar-core/inc/pulsar/ops.hpp) and keeps its argument meaning and its
  * precondition checks; the at::Tensor wrappers that keep the reference C++
@@ -33,6 +40,10 @@ typedef struct ihipStream_t* pw4_stream_t; /* == hipStream_t */
 #define PW4_ERR_WORKSPACE (-3) /* workspace missing or smaller than the *_workspace_size query */
 #define PW4_ERR_HIP (-4)       /* a HIP runtime call or kernel launch failed */
 #define PW4_ERR_GIDX (-5)      /* act-order g_idx is not a valid grouping */
+
+/* bytes at the start of every non-empty GEMM workspace that hold the K-split
+ * arrival counters (zero before first use, left zero by every call) */
+#define PW4_COUNTER_REGION_BYTES 65536
 
 /* element types */
 #define PW4_DTYPE_F16 0

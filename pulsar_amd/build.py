@@ -69,6 +69,14 @@ def _run_parallel(cmds: list[list[str]], verbose: bool) -> None:
         raise RuntimeError(f"build failed:\n{msg}")
 
 
+# Per-file extras.  The decode GEMM keeps its small MFMA accumulators in
+# VGPRs (no v_accvgpr moves around every 128-K step); the prefill GEMM needs
+# the AGPRs for its large accumulator tile.
+HIPCC_FILE_FLAGS = {
+    "gemm_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def build_hip(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     hipcc = _hipcc()
@@ -76,7 +84,8 @@ def build_hip(verbose: bool = False) -> str:
     for src in HIP_SOURCES:
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *HIPCC_FLAGS, *HIPCC_FILE_FLAGS.get(src, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+                     os.path.join(CSRC, src), "-o", obj])
     _run_parallel(cmds, verbose)
     out = os.path.join(HERE, LIB_NAME)
     tmp = out + ".tmp"

@@ -38,8 +38,13 @@ int cu_count() {
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-// Largest x slice a decode workgroup stages in LDS.
+// LDS budget of one decode workgroup when the library picks the K split
+// (four resident workgroups per CU), and the hard limit for a forced split.
+constexpr size_t kDecodeLdsAuto = 40 * 1024;
 constexpr size_t kDecodeLdsLimit = 64 * 1024;
+// Arrival counters of the decode K split: one int32 per 64-column block.
+constexpr size_t kCounterRegion = PW4_COUNTER_REGION_BYTES;
+constexpr int64_t kMaxCounterCols = (int64_t)(kCounterRegion / sizeof(int32_t));
 
 struct Plan {
     bool decode = false;
@@ -50,15 +55,14 @@ struct Plan {
     int splits = 1;
     size_t partial_bytes = 0;
     size_t xperm_bytes = 0;
-    size_t workspace() const { return align_up(partial_bytes) + align_up(xperm_bytes); }
+    // Every non-empty workspace starts with the fixed counter region, so the
+    // bytes a decode call uses as arrival counters are never scratch for
+    // another call that shares the workspace.
+    size_t workspace() const {
+        const size_t rest = align_up(partial_bytes) + align_up(xperm_bytes);
+        return rest ? kCounterRegion + rest : 0;
+    }
 };
-
-size_t decode_lds(int64_t M, int kps, int G) {
-    const size_t rs = (size_t)kps + 8;
-    const size_t x = (M * rs * 2 + 15) / 16 * 16;
-    const size_t ngl = (size_t)kps / (size_t)G + 2;
-    return x + (size_t)M * ngl * 4;
-}
 
 // layout: LAYOUT_MARLIN or LAYOUT_CT.  num_splits: 0 auto, >= 1 forced.
 Plan make_plan(int layout, int64_t M, int64_t N, int64_t K, int64_t G, bool has_perm, int64_t num_splits) {
@@ -67,7 +71,8 @@ Plan make_plan(int layout, int64_t M, int64_t N, int64_t K, int64_t G, bool has_
     const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
     const int64_t ktiles = kext / 32;
     const bool forced = num_splits >= 1;
-    const bool decode_ok = M <= 64 && (G == 64 || G % 128 == 0);
+    const bool zp_any = true;  // size the LDS for the asymmetric variant (a few hundred bytes more)
+    const bool decode_ok = M <= 64 && (G == 64 || G % 128 == 0) && (G & (G - 1)) == 0;
     if (decode_ok) {
         DecodeConfig dc{};
         dc.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
@@ -77,23 +82,27 @@ Plan make_plan(int layout, int64_t M, int64_t N, int64_t K, int64_t G, bool has_
         int64_t s;
         if (forced) {
             s = num_splits;
+        } else if (cols > kMaxCounterCols) {
+            s = 1;
         } else {
             const int64_t target = 2 * (int64_t)cus;
             s = std::min<int64_t>(std::max<int64_t>(ceil_div(target, std::max<int64_t>(cols, 1)), 1), steps);
         }
         int64_t kps = std::max<int64_t>(round_up(ceil_div(ktiles * 32, s), 128), 128);
         if (!forced) {
-            while (kps > 128 && decode_lds(M, (int)kps, (int)G) > kDecodeLdsLimit) kps -= 128;
+            while (kps > 128 && decode_lds_bytes((int)M, (int)kps, dc.ngrp, zp_any) > kDecodeLdsAuto) kps -= 128;
             s = std::max<int64_t>(ceil_div(ktiles * 32, kps), 1);
         }
         dc.k_per_split = (int)kps;
         dc.splits = (int)s;
-        dc.lds_bytes = decode_lds(M, (int)kps, (int)G);
-        if (dc.lds_bytes <= kDecodeLdsLimit) {
+        dc.lds_bytes = decode_lds_bytes((int)M, (int)kps, dc.ngrp, zp_any);
+        const bool partial = forced || s > 1;
+        if (dc.lds_bytes <= kDecodeLdsLimit && !(partial && cols > kMaxCounterCols)) {
             p.decode = true;
             p.dc = dc;
             p.splits = (int)s;
-            p.use_partial = forced || s > 1;
+            p.use_partial = partial;
+            if (partial) p.partial_bytes = (size_t)cols * s * M * 64 * sizeof(float);
         }
     }
     if (!p.decode) {
@@ -114,9 +123,9 @@ Plan make_plan(int layout, int64_t M, int64_t N, int64_t K, int64_t G, bool has_
         p.p_cps = (int)cps;
         p.splits = (int)s;
         p.use_partial = forced || s > 1;
+        if (p.use_partial) p.partial_bytes = (size_t)p.splits * M * N * 4;
         if (has_perm) p.xperm_bytes = (size_t)M * K * 2;
     }
-    if (p.use_partial) p.partial_bytes = (size_t)p.splits * M * N * 4;
     return p;
 }
 
@@ -135,8 +144,10 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
     const Plan p = make_plan(layout, M, N, K, G, perm != nullptr, num_splits);
     if (p.workspace() > 0 && (workspace == nullptr || ws_bytes < p.workspace())) return PW4_ERR_WORKSPACE;
     char* ws = reinterpret_cast<char*>(workspace);
-    float* partial = p.partial_bytes ? reinterpret_cast<float*>(ws) : nullptr;
-    uint16_t* xperm = p.xperm_bytes ? reinterpret_cast<uint16_t*>(ws + align_up(p.partial_bytes)) : nullptr;
+    int32_t* counters = p.workspace() ? reinterpret_cast<int32_t*>(ws) : nullptr;
+    float* partial = p.partial_bytes ? reinterpret_cast<float*>(ws + kCounterRegion) : nullptr;
+    uint16_t* xperm =
+        p.xperm_bytes ? reinterpret_cast<uint16_t*>(ws + kCounterRegion + align_up(p.partial_bytes)) : nullptr;
     const int xt = x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16;
     const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
     hipError_t e;
@@ -149,11 +160,13 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.perm = perm;
         a.y = reinterpret_cast<uint16_t*>(y);
         a.partial = p.use_partial ? partial : nullptr;
+        a.counters = counters;
         a.M = (int)M;
         a.N = (int)N;
         a.K = (int)K;
         a.G = (int)G;
         a.Kg = (int)(K / G);
+        a.G_log2 = (G & (G - 1)) == 0 ? __builtin_ctzll((unsigned long long)G) : -1;
         a.ktiles = (int)(kext / 32);
         a.nchunks = (int)(round_up(K, kMarlinBK) / kMarlinBK);
         a.k_per_split = p.dc.k_per_split;
@@ -188,7 +201,7 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         e = launch_prefill(layout, xt, stype, qzeros != nullptr, a, stream);
         if (e != hipSuccess) return hip_fail(e);
     }
-    if (p.use_partial) {
+    if (p.use_partial && !p.decode) {
         e = launch_combine(partial, reinterpret_cast<uint16_t*>(y), M * N, p.splits, xt, stream);
         if (e != hipSuccess) return hip_fail(e);
     }

@@ -10,6 +10,9 @@
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
 
+#include <map>
+#include <mutex>
+
 #include "pulsar_w4a16.h"
 
 namespace pulsar {
@@ -36,9 +39,26 @@ void check_status(int rc, const char* op) {
 
 int x_dtype_code(const at::Tensor& x) { return x.scalar_type() == at::kBFloat16 ? PW4_DTYPE_BF16 : PW4_DTYPE_F16; }
 
+// GEMM workspace: one per (device, stream), zero-filled when it is
+// allocated or grown, then reused.  The C ABI needs the counter region at its
+// start to be zero on entry and leaves it zero, and calls on one stream are
+// ordered, so sharing one workspace per stream is race free.
 at::Tensor workspace(size_t bytes, const at::Tensor& like) {
-    return at::empty({(int64_t)std::max<size_t>(bytes, 1)}, like.options().dtype(at::kByte));
+    if (bytes == 0) return at::Tensor();
+    static std::mutex mu;
+    static std::map<std::pair<int64_t, int64_t>, at::Tensor> cache;
+    const auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA();
+    const std::pair<int64_t, int64_t> key{like.device().index(), (int64_t)stream.id()};
+    std::lock_guard<std::mutex> lock(mu);
+    at::Tensor& t = cache[key];
+    if (!t.defined() || (size_t)t.numel() < bytes) {
+        const size_t grow = t.defined() ? std::max(bytes, (size_t)t.numel() * 2) : bytes;
+        t = at::zeros({(int64_t)grow}, like.options().dtype(at::kByte));
+    }
+    return t;
 }
+
+void* ptr_or_null(const at::Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }
 
 at::Tensor gemm_w4a16_run(const at::Tensor& x, const at::Tensor& weight_packed, const at::Tensor& weight_scale,
                           int64_t group_size, int64_t forced_splits) {
@@ -66,7 +86,7 @@ at::Tensor gemm_w4a16_run(const at::Tensor& x, const at::Tensor& weight_packed, 
     const size_t wsb = pw4_gemm_w4a16_workspace_size(M, N, K, group_size, forced_splits);
     at::Tensor wsp = workspace(wsb, x);
     const int rc = pw4_gemm_w4a16(x.data_ptr(), x_dtype_code(x), wp.data_ptr<int32_t>(), ws.data_ptr<float>(),
-                                  y.data_ptr(), M, N, K, group_size, forced_splits, wsp.data_ptr(), wsb,
+                                  y.data_ptr(), M, N, K, group_size, forced_splits, ptr_or_null(wsp), wsb,
                                   current_stream());
     check_status(rc, "gemm_w4a16");
     return y;
@@ -118,7 +138,7 @@ at::Tensor marlin_run(const at::Tensor& x, const at::Tensor& weight_marlin, cons
     at::Tensor wsp = workspace(wsb, x);
     const int rc = pw4_gemm_w4a16_marlin(x.data_ptr(), x_dtype_code(x), wm.data_ptr<int32_t>(), sm.data_ptr(),
                                          sm.scalar_type() == at::kFloat ? PW4_DTYPE_F32 : PW4_DTYPE_F16, zp, pp,
-                                         y.data_ptr(), M, N, K, group_size, forced_splits, wsp.data_ptr(), wsb,
+                                         y.data_ptr(), M, N, K, group_size, forced_splits, ptr_or_null(wsp), wsb,
                                          current_stream());
     check_status(rc, op);
     return y;

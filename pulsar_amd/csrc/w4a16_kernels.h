@@ -11,16 +11,20 @@ enum XType : int { X_F16 = 0, X_BF16 = 1 };
 enum SType : int { S_F32 = 0, S_F16 = 1 };
 
 // Decode GEMM (M <= 64): one workgroup = 4 waves = one 64-column block x one
-// K slice; wave w owns columns 16w..16w+15 of the block.
+// K slice; wave w owns columns 16w..16w+15 of the block.  With more than one
+// K slice, each workgroup writes an fp32 partial tile and the last one to
+// finish for a column block sums the partials in slice order and stores y.
 struct DecodeArgs {
     const uint16_t* x;       // [M, K] fp16 / bf16 bits
     const uint32_t* w;       // MARLIN words, or CT [N, K/8]
     const void* scales;      // MARLIN: [Kg, N]; CT: [N, Kg] fp32
     const uint32_t* qzeros;  // [Kg, N/8] (MARLIN, asymmetric) or null
     const int32_t* perm;     // [K] act-order gather of x, or null
-    uint16_t* y;             // [M, N] output when splits == 1
-    float* partial;          // [splits, M, N] fp32 when splits > 1
+    uint16_t* y;             // [M, N] output
+    float* partial;          // [cols, splits, M, 64] fp32, or null for the direct store
+    int32_t* counters;       // [cols] arrival counters (zero on entry, left zero)
     int M, N, K, G, Kg;
+    int G_log2;              // log2(G) when G is a power of two, else -1
     int ktiles;              // 32-wide K tiles present in the weight layout
     int nchunks;             // MARLIN: Kpad / 64
     int k_per_split;         // multiple of 128
@@ -35,6 +39,9 @@ struct DecodeConfig {
     int k_per_split;
     size_t lds_bytes;
 };
+
+// LDS bytes the decode kernel needs for an M x kps activation slice.
+size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp);
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          int grid_x, hipStream_t stream);
