@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "w4a16_common.h"
@@ -38,13 +39,21 @@ int cu_count() {
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-// LDS budget of one decode workgroup when the library picks the K split
-// (four resident workgroups per CU), and the hard limit for a forced split.
-constexpr size_t kDecodeLdsAuto = 40 * 1024;
-constexpr size_t kDecodeLdsLimit = 64 * 1024;
-// Arrival counters of the decode K split: one int32 per 64-column block.
+// LDS of one decode workgroup: the hard limit (160 KB per CU minus the
+// static part) and the per-CU capacity used to judge residency.
+constexpr size_t kDecodeLdsLimit = 152 * 1024;
+constexpr size_t kLdsPerCu = 160 * 1024;
+// Arrival counters of the decode K split: one int32 per workgroup column.
 constexpr size_t kCounterRegion = PW4_COUNTER_REGION_BYTES;
 constexpr int64_t kMaxCounterCols = (int64_t)(kCounterRegion / sizeof(int32_t));
+
+// Decode column width override (16, 32 or 64) for tuning sweeps; 0 = heuristic.
+int decode_nb_override() {
+    const char* e = std::getenv("PW4_DECODE_NB");
+    if (!e) return 0;
+    const int v = std::atoi(e);
+    return (v == 16 || v == 32 || v == 64) ? v : 0;
+}
 
 struct Plan {
     bool decode = false;
@@ -65,7 +74,8 @@ struct Plan {
 };
 
 // layout: LAYOUT_MARLIN or LAYOUT_CT.  num_splits: 0 auto, >= 1 forced.
-Plan make_plan(int layout, int64_t M, int64_t N, int64_t K, int64_t G, bool has_perm, int64_t num_splits) {
+Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N, int64_t K, int64_t G, bool has_perm,
+               int64_t num_splits) {
     Plan p;
     const int cus = cu_count();
     const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
@@ -77,32 +87,60 @@ Plan make_plan(int layout, int64_t M, int64_t N, int64_t K, int64_t G, bool has_
         DecodeConfig dc{};
         dc.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
         dc.ngrp = G == 64 ? 2 : 1;
-        const int64_t cols = layout == LAYOUT_MARLIN ? round_up(N, kMarlinBN) / 64 : ceil_div(N, 64);
+        const bool bf = x_dtype == PW4_DTYPE_BF16;
+        // Columns the units cover (MARLIN pads N to 64; CT columns past N are
+        // clamped loads whose results are dropped).
+        const int64_t ncols = layout == LAYOUT_MARLIN ? round_up(N, kMarlinBN) : round_up(N, 16);
         const int64_t steps = std::max<int64_t>(ceil_div(ktiles * 32, 128), 1);
-        int64_t s;
+        auto kps_for = [&](int64_t sp) { return std::max<int64_t>(round_up(ceil_div(ktiles * 32, sp), 128), 128); };
+        auto lds_for = [&](int64_t sp) { return decode_lds_bytes((int)M, (int)kps_for(sp), dc.ngrp, zp_any, bf); };
+        // K slices only when the activation slice does not fit in LDS: each
+        // slice costs a partial round trip per unit.
+        int64_t s = 1;
         if (forced) {
             s = num_splits;
-        } else if (cols > kMaxCounterCols) {
-            s = 1;
         } else {
-            const int64_t target = 2 * (int64_t)cus;
-            s = std::min<int64_t>(std::max<int64_t>(ceil_div(target, std::max<int64_t>(cols, 1)), 1), steps);
+            while (s < steps && lds_for(s) > kDecodeLdsLimit) ++s;
         }
-        int64_t kps = std::max<int64_t>(round_up(ceil_div(ktiles * 32, s), 128), 128);
-        if (!forced) {
-            while (kps > 128 && decode_lds_bytes((int)M, (int)kps, dc.ngrp, zp_any) > kDecodeLdsAuto) kps -= 128;
-            s = std::max<int64_t>(ceil_div(ktiles * 32, kps), 1);
+        const int64_t kps = kps_for(s);
+        if (!forced) s = std::max<int64_t>(ceil_div(ktiles * 32, kps), 1);
+        const size_t lds = lds_for(s);
+        // Units: 16 columns (eight K waves per strip, the finest balance), or
+        // 64 when K is sliced, to keep the per-unit partial round trips few.
+        int nb = decode_nb_override();
+        if (nb == 0) nb = s > 1 ? 64 : 16;
+        while (nb > 16 && ncols % nb != 0) nb /= 2;
+        const int64_t ncg = ceil_div(ncols, nb);
+        // Persistent grid: one or two workgroups per CU (register and LDS
+        // budget), then as few units per workgroup as possible with the
+        // least per-CU load.
+        int64_t per_cu_max =
+            lds <= kDecodeLdsLimit ? decode_blocks_per_cu(layout, bf ? X_BF16 : X_F16, stype, zp, dc.mt, dc.ngrp, lds) : 0;
+        if (per_cu_max <= 0) per_cu_max = std::max<int64_t>(std::min<int64_t>(2, (int64_t)(kLdsPerCu / std::max<size_t>(lds, 1))), 1);
+        per_cu_max = std::min<int64_t>(per_cu_max, 2);
+        int64_t best_wps = 1, best_cost = INT64_MAX;
+        for (int64_t per_cu = 1; per_cu <= per_cu_max; ++per_cu) {
+            const int64_t wps_max = std::max<int64_t>((int64_t)cus * per_cu / s, 1);
+            const int64_t ups = ceil_div(ncg, std::min(wps_max, ncg));
+            const int64_t wps = ceil_div(ncg, ups);
+            const int64_t cost = ups * ceil_div(wps * s, (int64_t)cus);
+            if (cost < best_cost || (cost == best_cost && wps > best_wps)) {
+                best_cost = cost;
+                best_wps = wps;
+            }
         }
+        dc.nb = nb;
+        dc.wps = (int)best_wps;
         dc.k_per_split = (int)kps;
         dc.splits = (int)s;
-        dc.lds_bytes = decode_lds_bytes((int)M, (int)kps, dc.ngrp, zp_any);
+        dc.lds_bytes = lds;
         const bool partial = forced || s > 1;
-        if (dc.lds_bytes <= kDecodeLdsLimit && !(partial && cols > kMaxCounterCols)) {
+        if (lds <= kDecodeLdsLimit && !(partial && ncg > kMaxCounterCols) && best_wps * s <= INT32_MAX) {
             p.decode = true;
             p.dc = dc;
             p.splits = (int)s;
             p.use_partial = partial;
-            if (partial) p.partial_bytes = (size_t)cols * s * M * 64 * sizeof(float);
+            if (partial) p.partial_bytes = (size_t)ncg * s * M * nb * sizeof(float);
         }
     }
     if (!p.decode) {
@@ -141,7 +179,7 @@ int check_common(int64_t M, int64_t N, int64_t K, int64_t G, int x_dtype) {
 int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const void* scales, int stype,
              const uint32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N, int64_t K, int64_t G,
              int64_t num_splits, void* workspace, size_t ws_bytes, hipStream_t stream) {
-    const Plan p = make_plan(layout, M, N, K, G, perm != nullptr, num_splits);
+    const Plan p = make_plan(layout, x_dtype, stype, qzeros != nullptr, M, N, K, G, perm != nullptr, num_splits);
     if (p.workspace() > 0 && (workspace == nullptr || ws_bytes < p.workspace())) return PW4_ERR_WORKSPACE;
     char* ws = reinterpret_cast<char*>(workspace);
     int32_t* counters = p.workspace() ? reinterpret_cast<int32_t*>(ws) : nullptr;
@@ -161,18 +199,22 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.y = reinterpret_cast<uint16_t*>(y);
         a.partial = p.use_partial ? partial : nullptr;
         a.counters = counters;
+        a.nb = p.dc.nb;
+        a.wps = p.dc.wps;
         a.M = (int)M;
         a.N = (int)N;
         a.K = (int)K;
         a.G = (int)G;
         a.Kg = (int)(K / G);
-        a.G_log2 = (G & (G - 1)) == 0 ? __builtin_ctzll((unsigned long long)G) : -1;
+        a.G_log2 = __builtin_ctzll((unsigned long long)G);
         a.ktiles = (int)(kext / 32);
         a.nchunks = (int)(round_up(K, kMarlinBK) / kMarlinBK);
         a.k_per_split = p.dc.k_per_split;
         a.rowstride = p.dc.k_per_split + 8;
         a.splits = p.dc.splits;
-        const int grid_x = (int)(layout == LAYOUT_MARLIN ? round_up(N, kMarlinBN) / 64 : ceil_div(N, 64));
+        const int64_t ncols = layout == LAYOUT_MARLIN ? round_up(N, kMarlinBN) : round_up(N, 16);
+        a.ncg = (int)ceil_div(ncols, p.dc.nb);
+        const int grid_x = p.dc.wps * p.dc.splits;
         e = launch_decode(layout, xt, stype, qzeros != nullptr, p.dc, a, grid_x, stream);
         if (e != hipSuccess) return hip_fail(e);
     } else {
@@ -259,7 +301,9 @@ int pw4_repack_w4a16(const int32_t* weight_packed, const void* weight_scale, int
 
 size_t pw4_gemm_w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group_size, int64_t num_splits) {
     if (check_common(M, N, K, group_size, PW4_DTYPE_F16) != PW4_OK || M == 0 || N == 0) return 0;
-    return make_plan(LAYOUT_CT, M, N, K, group_size, false, num_splits).workspace();
+    // the plan may differ by activation dtype (LDS budget): size for both
+    return std::max(make_plan(LAYOUT_CT, PW4_DTYPE_F16, S_F32, false, M, N, K, group_size, false, num_splits).workspace(),
+                    make_plan(LAYOUT_CT, PW4_DTYPE_BF16, S_F32, false, M, N, K, group_size, false, num_splits).workspace());
 }
 
 int pw4_gemm_w4a16(const void* x, int x_dtype, const int32_t* weight_packed, const float* weight_scale, void* y,
@@ -278,7 +322,9 @@ int pw4_gemm_w4a16(const void* x, int x_dtype, const int32_t* weight_packed, con
 size_t pw4_gemm_w4a16_marlin_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm,
                                             int64_t num_splits) {
     if (check_common(M, N, K, group_size, PW4_DTYPE_F16) != PW4_OK || M == 0 || N == 0) return 0;
-    return make_plan(LAYOUT_MARLIN, M, N, K, group_size, has_perm != 0, num_splits).workspace();
+    return std::max(
+        make_plan(LAYOUT_MARLIN, PW4_DTYPE_F16, S_F16, true, M, N, K, group_size, has_perm != 0, num_splits).workspace(),
+        make_plan(LAYOUT_MARLIN, PW4_DTYPE_BF16, S_F16, true, M, N, K, group_size, has_perm != 0, num_splits).workspace());
 }
 
 int pw4_gemm_w4a16_marlin(const void* x, int x_dtype, const int32_t* weight_marlin, const void* scales,

@@ -1,90 +1,138 @@
 // Memory-bound W4A16 GEMM for small M (decode): y[M,N] = x[M,K] @ dequant(W)^T.
 //
-// Work split.  grid.x walks 64-column blocks, grid.y walks K slices.  A
-// workgroup is 4 waves; wave w owns 16 output columns and streams its K slice
-// in 128-K steps.  Per step every lane issues ONE 16-byte global load: lane
+// Work split.  The weight matrix is cut into units of nb columns (16, 32 or
+// 64) and, when the activations of the whole K range do not fit in LDS, into
+// K slices.  Workgroups are persistent: gridDim.x = (workgroups per slice) x
+// slices, sized to what the CUs hold at once, and a workgroup loops over the
+// units of its slice (every wps-th unit).  A workgroup has 8 waves: nb/16
+// column waves, each owning a 16-column strip of the unit, times 8/(nb/16) K
+// waves that take interleaved 128-K steps of the slice and are summed through
+// LDS at the end of each unit.
+//
+// Streaming.  Per 128-K step every lane issues ONE 16-byte global load: lane
 // (c = l%16, h = l/16) fetches the four words of column c in 32-K tile h,
-// which are 16 contiguous bytes in both layouts, so a wave instruction reads
-// four fully used 256-byte segments (MARLIN).  The loads of the next U steps
-// sit in a register ring, and the first U are issued before the activations
-// are staged, so HBM latency overlaps the prologue.
+// which are 16 contiguous bytes in both layouts (MARLIN: a wave instruction
+// reads four fully used 256-byte segments).  The loads of the wave's next U
+// steps sit in a register ring that runs on across unit boundaries, so a unit
+// change costs no HBM round trip.  The activation slice is copied into LDS
+// once per workgroup with global_load_lds (no VGPRs), issued before the first
+// weight loads.
 //
-// Math.  The four words feed four v_mfma_f32_16x16x32.  B is the biased
-// integer form of the nibbles (1024 + u or 1024 + 16u in fp16, 128 + u in
-// bf16: two bitwise ops per pair, exact), and the activations of the 16u
-// slots are staged pre-multiplied by 1/16.  The bias and the zero point are
-// removed through the accumulator's initial value: every 128-K step starts
-// from -(bias * sum(a) + z * sum(a * w)) for its rows, computed in fp32 while
-// staging.  Each step's result is then scaled per column in fp32, so q * scale
-// is never rounded to 16 bits.
+// Math.  The four words feed four v_mfma_f32_16x16x32.  fp16: B = u - z
+// exactly (exponent splice of the nibble into 1024.0, then one packed add or
+// fma per pair), accumulated per 128-K step in fp32 and scaled per column in
+// fp32, so q * scale is never rounded to 16 bits.  bf16 has no cheap packed
+// subtract, so B = 128 + u (exact) and each step's accumulators start from
+// -(128 + z) * sum(x) of the step, summed from the staged slice.  The A
+// operand is read from LDS in the K order of the weight word: MARLIN word tg
+// of a 32-K tile holds dwords {tg, 4+tg, 8+tg, 12+tg} of the tile (two
+// ds_read2_b32); a compressed-tensors word holds 8 consecutive K, whose
+// nibble pairs are re-ordered with v_perm so A is a plain 16-byte read.
 //
-// K slices.  With more than one slice, every workgroup writes its fp32
-// partial tile, and the last workgroup to arrive for a column block (arrival
-// counter) sums the partials in slice order -- the fixed-order combine of the
-// reference (w4a16_common.cuh:94-120) without a second launch -- then resets
-// the counter to zero for the next call.
+// K slices across workgroups.  Every workgroup writes its fp32 partial tile
+// and the last to arrive for a unit (arrival counter) sums the partials in
+// slice order -- the fixed-order combine of the reference
+// (w4a16_common.cuh:94-120) without a second launch -- and resets the counter.
 //
 // Reference counterpart: w4a16_marlin_kernel / gemm_w4a16_kernel at BM = 16
 // (pulsar-core/src/kernels/w4a16_marlin.cu:197-304, w4a16_gemm.cu:153-264).
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "w4a16_common.h"
 #include "w4a16_kernels.h"
 
 namespace pw4 {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kRing = 8;
 
-// (a & mask) | (b & ~mask) in one v_bfi_b32.  gfx950 VOP3 takes no literal
-// operand, so the compiler would spend an AND and an OR on `(q & m) | c`;
-// here the mask lives in an SGPR and the splice constant in a VGPR.
-__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
-    uint32_t r;
-    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
-    return r;
+// (a & mask) | (b & ~mask).  The masks come from the kernel arguments (see
+// NibbleMasks) so the compiler cannot fold them into literals: gfx950 VOP3
+// takes no literal operand, and with two literal constants `(q & m) | c`
+// costs an AND and an OR; with the mask in an SGPR it is one v_bfi_b32 /
+// v_and_or_b32.  (Plain code, not inline assembly, so the compiler sees the
+// VGPR writes and inserts the wait states an MFMA reading them needs.)
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) { return (a & mask) | (b & ~mask); }
+
+// s_waitcnt vmcnt(n) leaving lgkmcnt / expcnt alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-// Biased B fragment of one weight word (see dq_f16_biased / dq_bf16_biased):
-// fp16 pairs 1024 + u (pairs 0, 2) and 1024 + 16u (pairs 1, 3); bf16 pairs
-// 128 + u.  `one` holds the splice constant (0x64006400 or 0x43004300).
-template <bool BF16, int LAYOUT>
-__device__ __forceinline__ u32x4 dq_biased(uint32_t q, uint32_t one) {
-    if constexpr (LAYOUT == LAYOUT_CT) q ^= 0x88888888u;  // two's complement -> u
+// fp16 B fragment = u - z, exact, for one weight word.  `one` = 0x64006400.
+//   MARLIN (unsigned nibbles): pairs (n_i, n_i+4), i = 0..3.
+//   CT (two's complement): pairs (n_2i, n_2i+1), i.e. natural K order.
+template <int LAYOUT>
+__device__ __forceinline__ u32x4 dq_f16(uint32_t q, uint32_t one, uint32_t z, const NibbleMasks& mk) {
+    const f16x2 z1024 = as_h2((0x6400u | z) * 0x10001u);                 // 1024 + z
+    const f16x2 z64 = as_h2((0x5400u | (z << 4)) * 0x10001u);             // 64 + z
+    const f16x2 sixteenth = as_h2(0x2c002c00u);
     u32x4 r;
-    if constexpr (BF16) {
-        r[0] = bfi(0x000f000fu, q, one);
-        r[1] = bfi(0x000f000fu, q >> 4, one);
-        r[2] = bfi(0x000f000fu, q >> 8, one);
-        r[3] = bfi(0x000f000fu, q >> 12, one);
-    } else {
+    if constexpr (LAYOUT == LAYOUT_MARLIN) {
         const uint32_t q8 = q >> 8;
-        r[0] = bfi(0x000f000fu, q, one);
-        r[1] = bfi(0x00f000f0u, q, one);
-        r[2] = bfi(0x000f000fu, q8, one);
-        r[3] = bfi(0x00f000f0u, q8, one);
+        r[0] = as_u32(as_h2(bfi(mk.lo, q, one)) - z1024);
+        r[1] = as_u32(as_h2(bfi(mk.hi, q, one)) * sixteenth - z64);
+        r[2] = as_u32(as_h2(bfi(mk.lo, q8, one)) - z1024);
+        r[3] = as_u32(as_h2(bfi(mk.hi, q8, one)) * sixteenth - z64);
+    } else {
+        q ^= 0x88888888u;  // two's complement -> u
+        const f16x2 mul = as_h2(0x2c003c00u);                                 // {1, 1/16}
+        const f16x2 sub = f16x2{z1024[0], z64[0]};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // byte i (nibbles 2i, 2i+1) into bytes 0 and 2, then splice
+            const uint32_t w = __builtin_amdgcn_perm(0u, q, 0x0c000c00u | (uint32_t)i | ((uint32_t)i << 16));
+            r[i] = as_u32(as_h2(bfi(mk.ct, w, one)) * mul - sub);
+        }
+    }
+    return r;
+}
+
+// bf16 B fragment = 128 + u (exact), same pair order as dq_f16.
+template <int LAYOUT>
+__device__ __forceinline__ u32x4 dq_bf16(uint32_t q, uint32_t one, const NibbleMasks& mk) {
+    u32x4 r;
+    if constexpr (LAYOUT == LAYOUT_MARLIN) {
+        r[0] = bfi(mk.lo, q, one);
+        r[1] = bfi(mk.lo, q >> 4, one);
+        r[2] = bfi(mk.lo, q >> 8, one);
+        r[3] = bfi(mk.lo, q >> 12, one);
+    } else {
+        q ^= 0x88888888u;
+        const uint32_t q4 = q >> 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // byte 0 = byte i of q (low nibble n_2i), byte 2 = byte i of q >> 4
+            // (low nibble n_2i+1), then splice both low nibbles
+            const uint32_t w = __builtin_amdgcn_perm(q4, q, 0x0c000c00u | (uint32_t)i | ((uint32_t)(4 + i) << 16));
+            r[i] = bfi(mk.lo, w, one);
+        }
     }
     return r;
 }
 
 template <bool BF16>
-__device__ __forceinline__ float half_lo(uint32_t d) {
+__device__ __forceinline__ float half_to_f32(uint16_t v) {
     if constexpr (BF16) {
-        return __builtin_bit_cast(float, d << 16);
+        return __builtin_bit_cast(float, (uint32_t)v << 16);
     } else {
-        return (float)as_h2(d)[0];
-    }
-}
-template <bool BF16>
-__device__ __forceinline__ float half_hi(uint32_t d) {
-    if constexpr (BF16) {
-        return __builtin_bit_cast(float, d & 0xffff0000u);
-    } else {
-        return (float)as_h2(d)[1];
+        return (float)__builtin_bit_cast(_Float16, v);
     }
 }
 
-// LDS layout: x rows [M][rowstride] halves, then CP and CQ, each
-// [steps][NGRP][MT*16] fp32 (CQ only with zero points).
-__host__ __device__ inline size_t x_bytes(int M, int rowstride) { return ((size_t)M * rowstride * 2 + 15) / 16 * 16; }
+// LDS layout (bytes from the start):
+//   X     [M][rowstride] halves, rowstride = kps + 8, padded to whole 1 KB
+//         copy blocks: the workgroup's activation slice in natural K order
+//   RED   [2][8 waves][MT*16][16] fp32: per-unit cross-wave sums, double buffered
+//   CP,CQ [steps][NGRP][MT*16] fp32: bf16 only, per-step correction terms
+__host__ __device__ inline size_t x_slots(int M, int kps) { return ((size_t)M * (kps / 8 + 1) + 63) / 64 * 64; }
+__host__ __device__ inline size_t red_floats(int mt) { return (size_t)2 * kWaves * mt * 16 * 16; }
 __host__ __device__ inline size_t corr_floats(int kps, int ngrp, int mt) { return (size_t)(kps / 128) * ngrp * mt * 16; }
 
 template <bool BF16, int LAYOUT, typename ST, int MT, int NGRP, bool ZP, int U>
@@ -92,54 +140,80 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     __shared__ int s_last;
     constexpr int MP = MT * 16;
-    constexpr float kBias = BF16 ? 128.f : 1024.f;
+    // vector memory instructions per ring step (weights, scales, zero points)
+    constexpr int kLoadsPerStep = 1 + NGRP + (ZP ? NGRP : 0);
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int c = lane & 15, h = lane >> 4;
-    const int cb = blockIdx.x;
-    const int split = blockIdx.y;
     const int M = a.M, N = a.N, K = a.K;
+    const int nb = a.nb;
+    const int cwn = nb >> 4;       // column waves
+    const int kwn = kWaves / cwn;  // K waves per 16-column strip
+    const int cw = wave % cwn, kw = wave / cwn;
+    const int split = blockIdx.x / a.wps;
+    const int wl = blockIdx.x - split * a.wps;
+    const int n_units = wl < a.ncg ? (a.ncg - wl + a.wps - 1) / a.wps : 0;
     const int rs = a.rowstride;
     const int kb = split * a.k_per_split;
     const int klen = max(min(kb + a.k_per_split, a.ktiles * 32) - kb, 0);  // multiple of 32
-    const int ntiles = klen / 32;
-    const int nsteps = (ntiles + 3) / 4;
+    const int nsteps = (klen / 32 + 3) / 4;
+    // Steps per unit, the same for every wave; at least one, so that an empty
+    // K slice still finishes its units (zero partials) and counts its arrival.
+    const int spu = max((nsteps + kwn - 1) / kwn, 1);
+    const int T = n_units * spu;
 
-    float* CP = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + x_bytes(M, rs));
+    float* RED = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + x_slots(M, a.k_per_split) * 16);
+    float* CP = RED + red_floats(MT);
     float* CQ = CP + corr_floats(a.k_per_split, NGRP, MT);
-
-    const int ncol = cb * 64 + wave * 16 + c;  // this lane's B column == D column
-    const bool col_ok = ncol < N;
-    const int ncol_c = min(ncol, N - 1);       // clamped: loads stay in bounds
     const ST* scales = reinterpret_cast<const ST*>(a.scales);
+    const uint32_t* smem32 = reinterpret_cast<const uint32_t*>(smem);
 
-    // Raw loaded values only: converting here would make the prefetch wait
-    // for its own loads.
+    // ---- the activation slice into LDS --------------------------------------
+    // 16-byte slots, row-major over [M][kps/8 + 1]; each wave instruction fills
+    // 64 consecutive slots (one global_load_lds_dwordx4).  Lanes whose slot is
+    // past K, past the slice or in the row pad are masked off: the copy never
+    // writes those slots, and the ones a step reads are zeroed below.
+    const int spr = a.k_per_split / 8 + 1;
+    const int nslots = (int)x_slots(M, a.k_per_split);
+    const int kvalid = max(min(klen, K - kb), 0);  // halves of real activations in the slice
+    const bool gather = a.perm != nullptr;
+    if (!gather) {
+        for (int b = wave; b * 64 < nslots; b += kWaves) {
+            const int f = b * 64 + lane;
+            const int row = f / spr, s8 = f - row * spr;
+            if (row < M && s8 * 8 < kvalid) {
+                __builtin_amdgcn_global_load_lds(a.x + (int64_t)row * K + kb + s8 * 8, smem + b * 512, 16, 0, 0);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- weight / scale / zero loads of the wave's t-th step ----------------
+    // Raw values only: converting here would make the prefetch wait for its
+    // own loads.  Positions past the wave's last step re-read it; steps past
+    // the slice (uneven K-wave split) load the slice's last step unused.
     struct Step {
         u32x4 w;
         ST s[NGRP];
         uint32_t z[NGRP];
     };
     const int gshift = a.G_log2;  // G is a power of two on this path
-
-    // Lane part of the MARLIN word offset inside one (column block, chunk
-    // pair); the chunk part is uniform and goes through scalar registers.
-    // A step that runs past the layout's last chunk (Kpad % 128 == 64) points
-    // its upper two tiles back at the last chunk: they meet zero activations.
-    const int loff = (h >> 1) * kChunkWords + (h & 1) * 256 + (wave * 16 + c) * 4;
-    const int loff_tail = (h & 1) * 256 + (wave * 16 + c) * 4;
-
-    // ---- weight / scale / zero loads of one 128-K step ----------------------
-    // Steps past the slice are clamped to its last step (a harmless re-read);
-    // tiles past the slice's end are multiplied by zero activations.
-    auto load_step = [&](int st, Step& o) {
-        st = min(st, max(nsteps - 1, 0));
+    const int lane_w = (h >> 1) * kChunkWords + (h & 1) * 256 + (cw * 16 + c) * 4;
+    const int lane_w_tail = (h & 1) * 256 + (cw * 16 + c) * 4;
+    auto load_step = [&](int u, int j, Step& o) {
+        if (u >= n_units) {
+            u = max(n_units - 1, 0);
+            j = spu - 1;
+        }
+        const int st = min(kw + j * kwn, max(nsteps - 1, 0));
         const int k0 = kb + st * 128;
+        const int col0 = (wl + u * a.wps) * nb;
+        const int ncol_c = min(col0 + cw * 16 + c, N - 1);
         if constexpr (LAYOUT == LAYOUT_MARLIN) {
-            const int kc = min(k0 >> 6, a.nchunks - 1);  // an empty slice reads the last chunk
-            const uint32_t* seg = a.w + ((int64_t)cb * a.nchunks + kc) * kChunkWords;
-            o.w = *reinterpret_cast<const u32x4*>(seg + (kc + 1 < a.nchunks ? loff : loff_tail));
+            const int kc = min(k0 >> 6, a.nchunks - 1);
+            const uint32_t* seg = a.w + ((int64_t)(col0 >> 6) * a.nchunks + kc) * kChunkWords + (col0 & 63) * 4;
+            o.w = *reinterpret_cast<const u32x4*>(seg + (kc + 1 < a.nchunks ? lane_w : lane_w_tail));
         } else {
             const int t = min(k0 / 32 + h, a.ktiles - 1);
             const int64_t off = (int64_t)ncol_c * (K / 8) + t * 4;
@@ -147,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
                 o.w = *reinterpret_cast<const u32x4*>(a.w + off);
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) o.w[j] = (t * 32 + j * 8 < K) ? a.w[off + j] : 0u;
+                for (int q = 0; q < 4; ++q) o.w[q] = (t * 32 + q * 8 < K) ? a.w[off + q] : 0u;
             }
         }
         const int g0 = k0 >> gshift;
@@ -164,119 +238,125 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     };
 
     Step ring[U];
-#pragma unroll
-    for (int i = 0; i < U; ++i) load_step(i, ring[i]);
-
-    // ---- stage x[0:M, kb:kb+klen] into LDS, permuted to the weight K order ---
-    // One item = one row x one 128-K step; it also produces the step's
-    // correction sums for that row.
-    for (int i = tid; i < M * nsteps; i += kThreads) {
-        const int m = i / nsteps, st = i - m * nsteps;
-        float P[NGRP], Q[NGRP];
-#pragma unroll
-        for (int gi = 0; gi < NGRP; ++gi) P[gi] = Q[gi] = 0.f;
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            const int tl = st * 4 + tt;
-            if (tl >= ntiles) {  // zero activations for tiles past the slice
-                u32x4* dst = reinterpret_cast<u32x4*>(smem + m * rs + tl * 32);
-#pragma unroll
-                for (int p = 0; p < 4; ++p) dst[p] = u32x4{0u, 0u, 0u, 0u};
-            } else {
-                const int k = kb + tl * 32;
-                u32x4 in[4];
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    const int kk = k + p * 8;
-                    if (a.perm) {
-                        uint16_t hv[8];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            hv[e] = (kk + e < K) ? a.x[(int64_t)m * K + min(max(a.perm[kk + e], 0), K - 1)]
-                                                 : (uint16_t)0;
-                        }
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) in[p][e] = (uint32_t)hv[2 * e] | ((uint32_t)hv[2 * e + 1] << 16);
-                    } else if (kk < K) {  // K % 8 == 0: pieces are all-in or all-out
-                        in[p] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * K + kk);
-                    } else {
-                        in[p] = u32x4{0u, 0u, 0u, 0u};
-                    }
-                }
-                u32x4 out[4];
-                permute_tile<LAYOUT>(in, out);
-                float sp = 0.f, sq = 0.f;
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) {
-                        if constexpr (!BF16) {
-                            if (d & 1) out[p][d] = as_u32(as_h2(out[p][d]) * as_h2(0x2c002c00u));  // x / 16
-                        }
-                        const float v = half_lo<BF16>(out[p][d]) + half_hi<BF16>(out[p][d]);
-                        sp += v;
-                        sq += (!BF16 && (d & 1)) ? 16.f * v : v;
-                    }
-                }
-                const int gi = NGRP == 1 ? 0 : tt / 2;
-                P[gi] += sp;
-                Q[gi] += sq;
-                u32x4* dst = reinterpret_cast<u32x4*>(smem + m * rs + tl * 32);
-#pragma unroll
-                for (int p = 0; p < 4; ++p) dst[p] = out[p];
-            }
+    int lu = 0, lj = 0;  // position of the next load
+    auto advance = [&](int& u, int& j) {
+        if (++j == spu) {
+            j = 0;
+            ++u;
         }
+    };
 #pragma unroll
-        for (int gi = 0; gi < NGRP; ++gi) {
-            const int idx = (st * NGRP + gi) * MP + m;
-            if constexpr (ZP) {
-                CP[idx] = -kBias * P[gi];
-                CQ[idx] = -Q[gi];
-            } else {
-                CP[idx] = -(kBias * P[gi] + 8.f * Q[gi]);
+    for (int i = 0; i < U; ++i) {
+        load_step(lu, lj, ring[i]);
+        advance(lu, lj);
+    }
+
+    // ---- finish the slice: act-order gather, zero fill, (bf16) corrections --
+    if (gather) {
+        for (int f = tid; f < nslots; f += kThreads) {
+            const int row = f / spr, s8 = f - row * spr;
+            u32x4 v = u32x4{0u, 0u, 0u, 0u};
+            if (row < M && s8 * 8 < kvalid) {
+                uint16_t hv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    hv[e] = a.x[(int64_t)row * K + min(max(a.perm[kb + s8 * 8 + e], 0), K - 1)];
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = (uint32_t)hv[2 * e] | ((uint32_t)hv[2 * e + 1] << 16);
             }
+            *reinterpret_cast<u32x4*>(smem + f * 8) = v;
+        }
+    } else {
+        if constexpr (LAYOUT == LAYOUT_MARLIN) {
+            wait_vmcnt<U * kLoadsPerStep>();  // this wave's slice copies are done; its ring is still in flight
+        } else {
+            wait_vmcnt<0>();
+        }
+        // zero the slots the last step reads past the real activations
+        const int zfrom = kvalid / 8, zto = nsteps * 16;
+        for (int i = tid; i < M * (zto - zfrom); i += kThreads) {
+            const int row = i / (zto - zfrom), s8 = zfrom + (i - row * (zto - zfrom));
+            *reinterpret_cast<u32x4*>(smem + (row * spr + s8) * 8) = u32x4{0u, 0u, 0u, 0u};
         }
     }
     __syncthreads();
+    if constexpr (BF16) {
+        // per-step corrections, stored negated: -(128 P + z Q) with P = Q = sum(x)
+        for (int i = tid; i < M * nsteps * NGRP; i += kThreads) {
+            const int m = i % M, sg = i / M, st = sg / NGRP, gi = sg - st * NGRP;
+            const int k0 = st * 128 + gi * (128 / NGRP), k1 = k0 + 128 / NGRP;
+            float p = 0.f;
+            for (int k = k0; k < k1; ++k) p += half_to_f32<true>(smem[m * rs + k]);
+            const int idx = (st * NGRP + gi) * MP + m;
+            if constexpr (ZP) {
+                CP[idx] = -128.f * p;
+                CQ[idx] = -p;
+            } else {
+                CP[idx] = -136.f * p;
+            }
+        }
+        __syncthreads();
+    }
 
+    // ---- main loop -----------------------------------------------------------
     f32x4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // A rows past M read row M-1 (their D rows are never stored); tiles past
-    // the slice read the zeros staged above.
     const uint32_t one = BF16 ? 0x43004300u : 0x64006400u;
-    int arow[MT];
+    int arow[MT];  // A rows past M read row M-1: their D rows are never stored
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) arow[mt] = min(mt * 16 + c, M - 1) * rs + 32 * h;
+    const int my_gi = NGRP == 1 ? 0 : h / 2;
 
-    auto compute_step = [&](int st, const Step& in) {
-        const int kl = st * 128;  // local K of the step
-        const int my_gi = NGRP == 1 ? 0 : h / 2;
+    auto compute_step = [&](int u, int j, const Step& in) {
+        const int st = kw + j * kwn;
+        if (st >= nsteps) return;  // uneven K-wave split: nothing here
+        const int kl = st * 128;
+        const int col0 = (wl + u * a.wps) * nb;
+        const int ncol_c = min(col0 + cw * 16 + c, N - 1);
+        uint32_t zl[NGRP];
+#pragma unroll
+        for (int gi = 0; gi < NGRP; ++gi) zl[gi] = ZP ? (in.z[gi] >> (4 * (ncol_c & 7))) & 0xfu : 8u;
         f32x4 tmp[NGRP][MT];
 #pragma unroll
-        for (int gi = 0; gi < NGRP; ++gi) {
-            float zf = 8.f;
-            if constexpr (ZP) zf = (float)((in.z[gi] >> (4 * (ncol_c & 7))) & 0xfu);
+        for (int gi = 0; gi < NGRP; ++gi)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const int idx = (st * NGRP + gi) * MP + mt * 16 + 4 * h;
-                const f32x4 cp = *reinterpret_cast<const f32x4*>(CP + idx);
-                if constexpr (ZP) {
-                    const f32x4 cq = *reinterpret_cast<const f32x4*>(CQ + idx);
+                if constexpr (BF16) {
+                    const int idx = (st * NGRP + gi) * MP + mt * 16 + 4 * h;
+                    const f32x4 cp = *reinterpret_cast<const f32x4*>(CP + idx);
+                    if constexpr (ZP) {
+                        const f32x4 cq = *reinterpret_cast<const f32x4*>(CQ + idx);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) tmp[gi][mt][j] = cp[j] + zf * cq[j];
+                        for (int r = 0; r < 4; ++r) tmp[gi][mt][r] = cp[r] + (float)zl[gi] * cq[r];
+                    } else {
+                        tmp[gi][mt] = cp;
+                    }
                 } else {
-                    tmp[gi][mt] = cp;
+                    tmp[gi][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
                 }
             }
-        }
+        uint32_t zsel = zl[0];
+#pragma unroll
+        for (int gi = 1; gi < NGRP; ++gi) zsel = my_gi == gi ? zl[gi] : zsel;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const u32x4 b = dq_biased<BF16, LAYOUT>(in.w[s], one);
+            u32x4 b;
+            if constexpr (BF16) {
+                b = dq_bf16<LAYOUT>(in.w[s], one, a.masks);
+            } else {
+                b = dq_f16<LAYOUT>(in.w[s], one, zsel, a.masks);
+            }
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const u32x4 av = *reinterpret_cast<const u32x4*>(smem + arow[mt] + kl + 8 * s);
+                u32x4 av;
+                if constexpr (LAYOUT == LAYOUT_MARLIN) {
+                    const uint32_t* p = smem32 + (arow[mt] + kl) / 2;
+                    av = u32x4{p[s], p[4 + s], p[8 + s], p[12 + s]};
+                } else {
+                    av = *reinterpret_cast<const u32x4*>(smem + arow[mt] + kl + 8 * s);
+                }
 #pragma unroll
                 for (int gi = 0; gi < NGRP; ++gi) {
                     u32x4 ag = av;
@@ -292,105 +372,128 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[mt][j] += load_scale(&in.s[gi]) * tmp[gi][mt][j];
+                for (int r = 0; r < 4; ++r) acc[mt][r] += load_scale(&in.s[gi]) * tmp[gi][mt][r];
+    };
+
+    // ---- end of a unit: sum the K waves in fixed order, store ----------------
+    int rbuf = 0;
+    auto finish_unit = [&](int u) {
+        float* red = RED + rbuf * (red_floats(MT) / 2);
+        rbuf ^= 1;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[(wave * MP + mt * 16 + 4 * h + r) * 16 + c] = acc[mt][r];
+            acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        __syncthreads();
+        const int cg = wl + u * a.wps;
+        const int col0 = cg * nb;
+        const int nout = M * nb;
+        auto reduced = [&](int i) {
+            const int row = i / nb, col = i - row * nb;
+            const int cwi = col >> 4, ci = col & 15;
+            float v = 0.f;
+            for (int k = 0; k < kwn; ++k) v += red[((k * cwn + cwi) * MP + row) * 16 + ci];
+            return v;
+        };
+        if (a.partial == nullptr) {
+            for (int i = tid; i < nout; i += kThreads) {
+                const int row = i / nb, n = col0 + (i - row * nb);
+                const float v = reduced(i);
+                if (n < N) a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
+            }
+            return;
+        }
+        // K slices across workgroups: the partials travel as device-scope
+        // atomic stores and loads (sc1: written through to, and read from, the
+        // device coherence point), the arrival counter is a device-scope
+        // atomic, and every wave waits for its partial stores to be
+        // acknowledged (vmcnt 0) before the barrier that precedes the counter
+        // increment, so whoever sees the last arrival also sees every partial.
+        // Agent-scope fences would be equivalent but write back the whole L2.
+        float* part = a.partial + ((int64_t)cg * a.splits + split) * nout;
+        for (int i = tid; i < nout; i += kThreads) {
+            __hip_atomic_store(part + i, reduced(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            s_last = __hip_atomic_fetch_add(a.counters + cg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     a.splits - 1;
+        }
+        __syncthreads();
+        if (s_last) {
+            const float* base = a.partial + (int64_t)cg * a.splits * nout;
+            for (int i = tid; i < nout; i += kThreads) {
+                float v = 0.f;
+                for (int sp = 0; sp < a.splits; ++sp) {
+                    v += __hip_atomic_load(base + (int64_t)sp * nout + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                const int row = i / nb, n = col0 + (i - row * nb);
+                if (n < N) a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
+            }
+            if (tid == 0) __hip_atomic_store(a.counters + cg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     };
 
     // Full blocks of U steps: unconditional refills (clamped past the end) so
     // the ring registers are written by the loads themselves, never through a
     // branch join that would force a wait.  Then the tail, without refills.
-    int st0 = 0;
-    for (; st0 + U <= nsteps; st0 += U) {
+    int cu = 0, cj = 0;  // position of the next compute
+    int t0 = 0;
+    for (; t0 + U <= T; t0 += U) {
 #pragma unroll
         for (int i = 0; i < U; ++i) {
-            compute_step(st0 + i, ring[i]);
-            load_step(st0 + i + U, ring[i]);
+            compute_step(cu, cj, ring[i]);
+            load_step(lu, lj, ring[i]);
+            advance(lu, lj);
             // keep the refill right behind its step: without the barrier the
             // scheduler batches all U computes first and drains the ring
             __builtin_amdgcn_sched_barrier(0);
+            if (cj == spu - 1) finish_unit(cu);
+            advance(cu, cj);
         }
     }
 #pragma unroll
     for (int i = 0; i < U; ++i) {
-        if (st0 + i < nsteps) compute_step(st0 + i, ring[i]);
-    }
-
-    // ---- epilogue: D lane holds column ncol, rows 16mt + 4h + j ------------
-    if (a.partial == nullptr) {
-        if (col_ok) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int row = mt * 16 + 4 * h + j;
-                    if (row < M) a.y[(int64_t)row * N + ncol] = f32_to_out<BF16>(acc[mt][j]);
-                }
+        if (t0 + i < T) {
+            compute_step(cu, cj, ring[i]);
+            if (cj == spu - 1) finish_unit(cu);
+            advance(cu, cj);
         }
-        return;
     }
-    // Cross-workgroup hand-off without an L2 write-back.  The partials travel
-    // as device-scope atomic stores and loads (sc1: written through to, and
-    // read from, the device coherence point), and the arrival counter is a
-    // device-scope atomic.  Every wave waits for its partial stores to be
-    // acknowledged (vmcnt 0) before the barrier that precedes the counter
-    // increment, so whoever sees the last arrival also sees every partial.
-    // Agent-scope fences would be equivalent but write back the whole L2.
-    float* part = a.partial + ((int64_t)cb * a.splits + split) * M * 64;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = mt * 16 + 4 * h + j;
-            if (row < M)
-                __hip_atomic_store(part + row * 64 + wave * 16 + c, acc[mt][j], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        s_last = __hip_atomic_fetch_add(a.counters + cb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 a.splits - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    const float* base = a.partial + (int64_t)cb * a.splits * M * 64;
-    for (int i = tid; i < M * 64; i += kThreads) {
-        float s = 0.f;
-        for (int sp = 0; sp < a.splits; ++sp) {
-            s += __hip_atomic_load(base + (int64_t)sp * M * 64 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        const int row = i >> 6, col = cb * 64 + (i & 63);
-        if (col < N) a.y[(int64_t)row * N + col] = f32_to_out<BF16>(s);
-    }
-    if (tid == 0) __hip_atomic_store(a.counters + cb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-constexpr int kRing = 8;
-
-template <bool BF16, int LAYOUT, typename ST, int MT, int NGRP, bool ZP>
-hipError_t launch_one(const DecodeConfig& cfg, const DecodeArgs& a, int grid_x, hipStream_t stream) {
-    auto kern = decode_kernel<BF16, LAYOUT, ST, MT, NGRP, ZP, kRing>;
-    if (cfg.lds_bytes > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)cfg.lds_bytes);
-        if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(kern, dim3(grid_x, cfg.splits), dim3(kThreads), cfg.lds_bytes, stream, a);
-    return hipGetLastError();
-}
+using DecodeFn = void (*)(const DecodeArgs);
 
 template <bool BF16, int LAYOUT, typename ST, bool ZP>
-hipError_t launch_mt(const DecodeConfig& cfg, const DecodeArgs& a, int grid_x, hipStream_t stream) {
-#define PW4_NGRP(MT_)                                                                               \
-    if (cfg.ngrp == 1) return launch_one<BF16, LAYOUT, ST, MT_, 1, ZP>(cfg, a, grid_x, stream); \
-    if (cfg.ngrp == 2) return launch_one<BF16, LAYOUT, ST, MT_, 2, ZP>(cfg, a, grid_x, stream); \
-    return hipErrorInvalidValue;
-    switch (cfg.mt) {
-        case 1: { PW4_NGRP(1) }
-        case 2: { PW4_NGRP(2) }
-        case 4: { PW4_NGRP(4) }
-        default: return hipErrorInvalidValue;
+DecodeFn pick_mt(int mt, int ngrp) {
+    if (mt == 1) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 1, 1, ZP, kRing> : decode_kernel<BF16, LAYOUT, ST, 1, 2, ZP, kRing>;
+    if (mt == 2) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 2, 1, ZP, kRing> : decode_kernel<BF16, LAYOUT, ST, 2, 2, ZP, kRing>;
+    if (mt == 4) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 4, 1, ZP, kRing> : decode_kernel<BF16, LAYOUT, ST, 4, 2, ZP, kRing>;
+    return nullptr;
+}
+
+template <bool BF16>
+DecodeFn pick_layout(int layout, int stype, bool zp, int mt, int ngrp) {
+    if (layout == LAYOUT_CT) return (zp || stype != S_F32) ? nullptr : pick_mt<BF16, LAYOUT_CT, float, false>(mt, ngrp);
+    if (stype == S_F32) {
+        return zp ? pick_mt<BF16, LAYOUT_MARLIN, float, true>(mt, ngrp)
+                  : pick_mt<BF16, LAYOUT_MARLIN, float, false>(mt, ngrp);
     }
-#undef PW4_NGRP
+    return zp ? pick_mt<BF16, LAYOUT_MARLIN, _Float16, true>(mt, ngrp)
+              : pick_mt<BF16, LAYOUT_MARLIN, _Float16, false>(mt, ngrp);
+}
+
+DecodeFn pick_decode(int layout, int xtype, int stype, bool zp, int mt, int ngrp) {
+    return xtype == X_BF16 ? pick_layout<true>(layout, stype, zp, mt, ngrp)
+                           : pick_layout<false>(layout, stype, zp, mt, ngrp);
+}
+
+hipError_t prepare(DecodeFn fn, size_t lds) {
+    if (lds <= 64 * 1024) return hipSuccess;
+    return hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
 }
 
 // Fixed-order sum of [splits, M, N] fp32 partials, then the cast to y's dtype
@@ -418,33 +521,47 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 
 }  // namespace
 
-size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp) {
+size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16) {
     const int mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-    return x_bytes(M, kps + 8) + corr_floats(kps, ngrp, mt) * 4 * (zp ? 2 : 1);
+    size_t b = x_slots(M, kps) * 16 + red_floats(mt) * 4;
+    if (bf16) b += corr_floats(kps, ngrp, mt) * 4 * (zp ? 2 : 1);
+    return b;
+}
+
+int decode_threads() { return kThreads; }
+
+int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, size_t lds) {
+    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, mt, ngrp);
+    if (fn == nullptr) return 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    static std::mutex mu;
+    static std::map<std::tuple<int, const void*, size_t>, int> cache;
+    const auto key = std::make_tuple(dev, (const void*)fn, lds);
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        auto it = cache.find(key);
+        if (it != cache.end()) return it->second;
+    }
+    int n = 0;
+    if (prepare(fn, lds) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void*)fn, kThreads, lds) != hipSuccess) {
+        (void)hipGetLastError();  // do not leave the failure for the next launch check to report
+        return 0;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    cache[key] = n;
+    return n;
 }
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          int grid_x, hipStream_t stream) {
-    const bool bf = xtype == X_BF16;
-    if (layout == LAYOUT_CT) {
-        if (zp || stype != S_F32) return hipErrorInvalidValue;
-        return bf ? launch_mt<true, LAYOUT_CT, float, false>(cfg, a, grid_x, stream)
-                  : launch_mt<false, LAYOUT_CT, float, false>(cfg, a, grid_x, stream);
-    }
-    if (stype == S_F32) {
-        if (zp) {
-            return bf ? launch_mt<true, LAYOUT_MARLIN, float, true>(cfg, a, grid_x, stream)
-                      : launch_mt<false, LAYOUT_MARLIN, float, true>(cfg, a, grid_x, stream);
-        }
-        return bf ? launch_mt<true, LAYOUT_MARLIN, float, false>(cfg, a, grid_x, stream)
-                  : launch_mt<false, LAYOUT_MARLIN, float, false>(cfg, a, grid_x, stream);
-    }
-    if (zp) {
-        return bf ? launch_mt<true, LAYOUT_MARLIN, _Float16, true>(cfg, a, grid_x, stream)
-                  : launch_mt<false, LAYOUT_MARLIN, _Float16, true>(cfg, a, grid_x, stream);
-    }
-    return bf ? launch_mt<true, LAYOUT_MARLIN, _Float16, false>(cfg, a, grid_x, stream)
-              : launch_mt<false, LAYOUT_MARLIN, _Float16, false>(cfg, a, grid_x, stream);
+    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp);
+    if (fn == nullptr) return hipErrorInvalidValue;
+    hipError_t e = prepare(fn, cfg.lds_bytes);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(fn, dim3(grid_x), dim3(kThreads), cfg.lds_bytes, stream, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_combine(const float* partial, uint16_t* y, int64_t mn, int splits, int xtype,

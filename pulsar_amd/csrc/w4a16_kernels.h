@@ -10,10 +10,20 @@ namespace pw4 {
 enum XType : int { X_F16 = 0, X_BF16 = 1 };
 enum SType : int { S_F32 = 0, S_F16 = 1 };
 
-// Decode GEMM (M <= 64): one workgroup = 4 waves = one 64-column block x one
-// K slice; wave w owns columns 16w..16w+15 of the block.  With more than one
-// K slice, each workgroup writes an fp32 partial tile and the last one to
-// finish for a column block sums the partials in slice order and stores y.
+// Decode GEMM (M <= 64).  The columns are cut into units of nb (16, 32 or
+// 64) and K into `splits` slices; gridDim.x = wps * splits persistent
+// workgroups of 8 waves, workgroup w taking slice w / wps and the units
+// w % wps, w % wps + wps, ...  With more than one slice, each workgroup writes
+// an fp32 partial tile per unit and the last one to finish a unit sums the
+// partials in slice order and stores y.
+// Nibble masks for the exponent-splice dequant, passed at run time so the
+// compiler keeps them in SGPRs (see bfi in gemm_decode.hip).
+struct NibbleMasks {
+    uint32_t lo = 0x000f000fu;  // nibbles 0 and 4 of a word
+    uint32_t hi = 0x00f000f0u;  // nibbles 1 and 5
+    uint32_t ct = 0x00f0000fu;  // low nibble of byte 0, high nibble of byte 2
+};
+
 struct DecodeArgs {
     const uint16_t* x;       // [M, K] fp16 / bf16 bits
     const uint32_t* w;       // MARLIN words, or CT [N, K/8]
@@ -21,27 +31,38 @@ struct DecodeArgs {
     const uint32_t* qzeros;  // [Kg, N/8] (MARLIN, asymmetric) or null
     const int32_t* perm;     // [K] act-order gather of x, or null
     uint16_t* y;             // [M, N] output
-    float* partial;          // [cols, splits, M, 64] fp32, or null for the direct store
-    int32_t* counters;       // [cols] arrival counters (zero on entry, left zero)
+    float* partial;          // [ncg, splits, M, nb] fp32, or null for the direct store
+    int32_t* counters;       // [ncg] arrival counters (zero on entry, left zero)
+    int nb;                  // columns per unit: 16, 32 or 64
+    int ncg;                 // units (column groups) per slice
+    int wps;                 // workgroups per slice
     int M, N, K, G, Kg;
-    int G_log2;              // log2(G) when G is a power of two, else -1
+    int G_log2;              // log2(G); G is a power of two on this path
     int ktiles;              // 32-wide K tiles present in the weight layout
     int nchunks;             // MARLIN: Kpad / 64
     int k_per_split;         // multiple of 128
-    int rowstride;           // LDS row stride of the staged x, in halves
+    int rowstride;           // LDS row stride of the staged x, in halves (k_per_split + 8)
     int splits;
+    NibbleMasks masks;
 };
 
 struct DecodeConfig {
+    int nb;      // columns per unit
+    int wps;     // workgroups per K slice
     int mt;      // 16-row M tiles per wave (1, 2, 4)
     int ngrp;    // quant groups per 128-K step (1 when G % 128 == 0, 2 when G == 64)
-    int splits;  // K slices (grid.y)
+    int splits;  // K slices
     int k_per_split;
     size_t lds_bytes;
 };
 
-// LDS bytes the decode kernel needs for an M x kps activation slice.
-size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp);
+// LDS bytes of one decode workgroup for an M x kps activation slice, and its
+// thread count.
+size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16);
+int decode_threads();
+// Resident decode workgroups per CU for the kernel variant and LDS size
+// (0 when the variant does not exist or the runtime cannot tell).
+int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, size_t lds);
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          int grid_x, hipStream_t stream);
