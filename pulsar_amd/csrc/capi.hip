@@ -111,11 +111,16 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         if (nb == 0) nb = s > 1 ? 64 : 16;
         while (nb > 16 && ncols % nb != 0) nb /= 2;
         const int64_t ncg = ceil_div(ncols, nb);
+        // ring depth: a unit of at most 4 steps per wave needs no more (its
+        // steps pad to the ring depth)
+        const int64_t kwn = 8 / (nb / 16);
+        const int64_t spu = std::max<int64_t>(ceil_div(ceil_div(kps, 128), kwn), 1);
+        dc.ring = spu <= 4 ? 4 : 8;
         // Persistent grid: one or two workgroups per CU (register and LDS
         // budget), then as few units per workgroup as possible with the
         // least per-CU load.
         int64_t per_cu_max =
-            lds <= kDecodeLdsLimit ? decode_blocks_per_cu(layout, bf ? X_BF16 : X_F16, stype, zp, dc.mt, dc.ngrp, lds) : 0;
+            lds <= kDecodeLdsLimit ? decode_blocks_per_cu(layout, bf ? X_BF16 : X_F16, stype, zp, dc.mt, dc.ngrp, dc.ring, lds) : 0;
         if (per_cu_max <= 0) per_cu_max = std::max<int64_t>(std::min<int64_t>(2, (int64_t)(kLdsPerCu / std::max<size_t>(lds, 1))), 1);
         per_cu_max = std::min<int64_t>(per_cu_max, 2);
         int64_t best_wps = 1, best_cost = INT64_MAX;

@@ -23,11 +23,12 @@
 // fma per pair), accumulated per 128-K step in fp32 and scaled per column in
 // fp32, so q * scale is never rounded to 16 bits.  bf16 has no cheap packed
 // subtract, so B = 128 + u (exact) and each step's accumulators start from
-// -(128 + z) * sum(x) of the step, summed from the staged slice.  The A
-// operand is read from LDS in the K order of the weight word: MARLIN word tg
-// of a 32-K tile holds dwords {tg, 4+tg, 8+tg, 12+tg} of the tile (two
-// ds_read2_b32); a compressed-tensors word holds 8 consecutive K, whose
-// nibble pairs are re-ordered with v_perm so A is a plain 16-byte read.
+// -(128 + z) * sum(x) of the step, summed from the staged slice.  The
+// activations stay in natural K order: MARLIN word tg of a 32-K tile holds
+// K {8p + 2tg, 8p + 2tg + 1} in its nibble pair p, so pair s of the tile's
+// four words is the contiguous run [8s, 8s + 8) that MFMA s multiplies; a
+// compressed-tensors word is such a run already (its pairs re-ordered with
+// v_perm).  Either way the A operand is one 16-byte LDS read.
 //
 // K slices across workgroups.  Every workgroup writes its fp32 partial tile
 // and the last to arrive for a unit (arrival counter) sums the partials in
@@ -50,13 +51,12 @@ constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kRing = 8;
 
-// (a & mask) | (b & ~mask).  The masks come from the kernel arguments (see
-// NibbleMasks) so the compiler cannot fold them into literals: gfx950 VOP3
-// takes no literal operand, and with two literal constants `(q & m) | c`
-// costs an AND and an OR; with the mask in an SGPR it is one v_bfi_b32 /
-// v_and_or_b32.  (Plain code, not inline assembly, so the compiler sees the
-// VGPR writes and inserts the wait states an MFMA reading them needs.)
-__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) { return (a & mask) | (b & ~mask); }
+// (a & mask) | b for a splice constant b with no bits under the mask.  The
+// masks come from the kernel arguments (see NibbleMasks) and b from a VGPR,
+// so the compiler cannot fold them into literals (gfx950 VOP3 takes none) and
+// emits one v_and_or_b32.  Plain code, not inline assembly: the compiler sees
+// the VGPR write and inserts the wait states an MFMA reading it needs.
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) { return (a & mask) | b; }
 
 // s_waitcnt vmcnt(n) leaving lgkmcnt / expcnt alone (gfx9 encoding).
 template <int N>
@@ -144,7 +144,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     constexpr int kLoadsPerStep = 1 + NGRP + (ZP ? NGRP : 0);
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    // wave-uniform by construction; readfirstlane tells the compiler, so that
+    // everything derived from it (K wave, unit columns, step bookkeeping) is
+    // scalar arithmetic and scalar branches
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
     const int c = lane & 15, h = lane >> 4;
     const int M = a.M, N = a.N, K = a.K;
     const int nb = a.nb;
@@ -161,19 +165,20 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     // Steps per unit, the same for every wave; at least one, so that an empty
     // K slice still finishes its units (zero partials) and counts its arrival.
     const int spu = max((nsteps + kwn - 1) / kwn, 1);
-    const int T = n_units * spu;
+    const int spu_pad = (spu + U - 1) / U * U;  // positions per unit, a whole number of ring blocks
 
     float* RED = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + x_slots(M, a.k_per_split) * 16);
     float* CP = RED + red_floats(MT);
     float* CQ = CP + corr_floats(a.k_per_split, NGRP, MT);
     const ST* scales = reinterpret_cast<const ST*>(a.scales);
-    const uint32_t* smem32 = reinterpret_cast<const uint32_t*>(smem);
 
     // ---- the activation slice into LDS --------------------------------------
-    // 16-byte slots, row-major over [M][kps/8 + 1]; each wave instruction fills
-    // 64 consecutive slots (one global_load_lds_dwordx4).  Lanes whose slot is
-    // past K, past the slice or in the row pad are masked off: the copy never
-    // writes those slots, and the ones a step reads are zeroed below.
+    // 16-byte slots, row-major over [M][kps/8 + 1] in natural K order (the
+    // last slot of a row is padding); each wave instruction fills 64
+    // consecutive slots (one global_load_lds_dwordx4) from per-lane global
+    // addresses.  Lanes whose slot is past K, past the slice or in the pad are
+    // masked off: the copy never writes those slots, and the ones a step
+    // reads are zeroed below.
     const int spr = a.k_per_split / 8 + 1;
     const int nslots = (int)x_slots(M, a.k_per_split);
     const int kvalid = max(min(klen, K - kb), 0);  // halves of real activations in the slice
@@ -206,6 +211,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
             u = max(n_units - 1, 0);
             j = spu - 1;
         }
+        j = min(j, spu - 1);  // padding positions re-read the unit's last step
         const int st = min(kw + j * kwn, max(nsteps - 1, 0));
         const int k0 = kb + st * 128;
         const int col0 = (wl + u * a.wps) * nb;
@@ -238,21 +244,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     };
 
     Step ring[U];
-    int lu = 0, lj = 0;  // position of the next load
-    auto advance = [&](int& u, int& j) {
-        if (++j == spu) {
-            j = 0;
-            ++u;
-        }
-    };
 #pragma unroll
-    for (int i = 0; i < U; ++i) {
-        load_step(lu, lj, ring[i]);
-        advance(lu, lj);
-    }
+    for (int i = 0; i < U; ++i) load_step(0, i, ring[i]);
 
     // ---- finish the slice: act-order gather, zero fill, (bf16) corrections --
     if (gather) {
+        // act-order: element gathers through registers, one slot per item
         for (int f = tid; f < nslots; f += kThreads) {
             const int row = f / spr, s8 = f - row * spr;
             u32x4 v = u32x4{0u, 0u, 0u, 0u};
@@ -273,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
         } else {
             wait_vmcnt<0>();
         }
-        // zero the slots the last step reads past the real activations
+        // zero the slots the steps read past the real activations
         const int zfrom = kvalid / 8, zto = nsteps * 16;
         for (int i = tid; i < M * (zto - zfrom); i += kThreads) {
             const int row = i / (zto - zfrom), s8 = zfrom + (i - row * (zto - zfrom));
@@ -303,7 +300,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     f32x4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint32_t one = BF16 ? 0x43004300u : 0x64006400u;
+    // The splice constant in a VGPR (the masks come in SGPRs): one VOP3 may
+    // read a single SGPR, so this is what lets `(q & m) | c` be one
+    // v_and_or_b32.  The move is opaque so the constant is not re-folded.
+    uint32_t one;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(one) : "s"(BF16 ? 0x43004300u : 0x64006400u));
     int arow[MT];  // A rows past M read row M-1: their D rows are never stored
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) arow[mt] = min(mt * 16 + c, M - 1) * rs + 32 * h;
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
 
     auto compute_step = [&](int u, int j, const Step& in) {
         const int st = kw + j * kwn;
-        if (st >= nsteps) return;  // uneven K-wave split: nothing here
+        if (j >= spu || st >= nsteps) return;  // padding, or an uneven K-wave split
         const int kl = st * 128;
         const int col0 = (wl + u * a.wps) * nb;
         const int ncol_c = min(col0 + cw * 16 + c, N - 1);
@@ -340,23 +341,30 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
         uint32_t zsel = zl[0];
 #pragma unroll
         for (int gi = 1; gi < NGRP; ++gi) zsel = my_gi == gi ? zl[gi] : zsel;
+        // MARLIN: pair s of word tg holds natural K 8s + 2tg, 8s + 2tg + 1, so
+        // pair s of the four words is the contiguous K run [8s, 8s + 8) of the
+        // tile, which MFMA s multiplies with natural-order activations.  CT:
+        // word s is that run already (dq_* emits its pairs in K order).
+        u32x4 d[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            if constexpr (BF16) {
+                d[w] = dq_bf16<LAYOUT>(in.w[w], one, a.masks);
+            } else {
+                d[w] = dq_f16<LAYOUT>(in.w[w], one, zsel, a.masks);
+            }
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             u32x4 b;
-            if constexpr (BF16) {
-                b = dq_bf16<LAYOUT>(in.w[s], one, a.masks);
+            if constexpr (LAYOUT == LAYOUT_MARLIN) {
+                b = u32x4{d[0][s], d[1][s], d[2][s], d[3][s]};
             } else {
-                b = dq_f16<LAYOUT>(in.w[s], one, zsel, a.masks);
+                b = d[s];
             }
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                u32x4 av;
-                if constexpr (LAYOUT == LAYOUT_MARLIN) {
-                    const uint32_t* p = smem32 + (arow[mt] + kl) / 2;
-                    av = u32x4{p[s], p[4 + s], p[8 + s], p[12 + s]};
-                } else {
-                    av = *reinterpret_cast<const u32x4*>(smem + arow[mt] + kl + 8 * s);
-                }
+                const u32x4 av = *reinterpret_cast<const u32x4*>(smem + arow[mt] + kl + 8 * s);
 #pragma unroll
                 for (int gi = 0; gi < NGRP; ++gi) {
                     u32x4 ag = av;
@@ -437,58 +445,60 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
         }
     };
 
-    // Full blocks of U steps: unconditional refills (clamped past the end) so
-    // the ring registers are written by the loads themselves, never through a
-    // branch join that would force a wait.  Then the tail, without refills.
-    int cu = 0, cj = 0;  // position of the next compute
-    int t0 = 0;
-    for (; t0 + U <= T; t0 += U) {
+    // Unit-major loop.  A unit's steps are padded to a multiple of U, so unit
+    // boundaries fall on ring-block boundaries: one copy of the unit epilogue,
+    // and the ring slots stay compile-time.  Refills are unconditional
+    // (clamped past the end) so the ring registers are written by the loads
+    // themselves, never through a branch join that would force a wait.
+    for (int u = 0; u < n_units; ++u) {
+        for (int jb = 0; jb < spu_pad; jb += U) {
+            // this block's refills: the next block of the unit, or the next
+            // unit's first block
+            const bool same = jb + U < spu_pad;
+            const int tu = same ? u : u + 1, tj = same ? jb + U : 0;
 #pragma unroll
-        for (int i = 0; i < U; ++i) {
-            compute_step(cu, cj, ring[i]);
-            load_step(lu, lj, ring[i]);
-            advance(lu, lj);
-            // keep the refill right behind its step: without the barrier the
-            // scheduler batches all U computes first and drains the ring
-            __builtin_amdgcn_sched_barrier(0);
-            if (cj == spu - 1) finish_unit(cu);
-            advance(cu, cj);
+            for (int i = 0; i < U; ++i) {
+                compute_step(u, jb + i, ring[i]);
+                load_step(tu, tj + i, ring[i]);
+                // keep the refill right behind its step: without the barrier
+                // the scheduler batches all U computes first and drains the ring
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-    }
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-        if (t0 + i < T) {
-            compute_step(cu, cj, ring[i]);
-            if (cj == spu - 1) finish_unit(cu);
-            advance(cu, cj);
-        }
+        finish_unit(u);
     }
 }
 
 using DecodeFn = void (*)(const DecodeArgs);
 
-template <bool BF16, int LAYOUT, typename ST, bool ZP>
-DecodeFn pick_mt(int mt, int ngrp) {
-    if (mt == 1) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 1, 1, ZP, kRing> : decode_kernel<BF16, LAYOUT, ST, 1, 2, ZP, kRing>;
-    if (mt == 2) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 2, 1, ZP, kRing> : decode_kernel<BF16, LAYOUT, ST, 2, 2, ZP, kRing>;
-    if (mt == 4) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 4, 1, ZP, kRing> : decode_kernel<BF16, LAYOUT, ST, 4, 2, ZP, kRing>;
+template <bool BF16, int LAYOUT, typename ST, bool ZP, int U>
+DecodeFn pick_mt_u(int mt, int ngrp) {
+    if (mt == 1) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 1, 1, ZP, U> : decode_kernel<BF16, LAYOUT, ST, 1, 2, ZP, U>;
+    if (mt == 2) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 2, 1, ZP, U> : decode_kernel<BF16, LAYOUT, ST, 2, 2, ZP, U>;
+    if (mt == 4) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 4, 1, ZP, U> : decode_kernel<BF16, LAYOUT, ST, 4, 2, ZP, U>;
     return nullptr;
 }
 
-template <bool BF16>
-DecodeFn pick_layout(int layout, int stype, bool zp, int mt, int ngrp) {
-    if (layout == LAYOUT_CT) return (zp || stype != S_F32) ? nullptr : pick_mt<BF16, LAYOUT_CT, float, false>(mt, ngrp);
-    if (stype == S_F32) {
-        return zp ? pick_mt<BF16, LAYOUT_MARLIN, float, true>(mt, ngrp)
-                  : pick_mt<BF16, LAYOUT_MARLIN, float, false>(mt, ngrp);
-    }
-    return zp ? pick_mt<BF16, LAYOUT_MARLIN, _Float16, true>(mt, ngrp)
-              : pick_mt<BF16, LAYOUT_MARLIN, _Float16, false>(mt, ngrp);
+// ring depth: 4 steps when a unit has at most 4 per wave (no padding), else 8
+template <bool BF16, int LAYOUT, typename ST, bool ZP>
+DecodeFn pick_mt(int mt, int ngrp, int ring) {
+    return ring == 4 ? pick_mt_u<BF16, LAYOUT, ST, ZP, 4>(mt, ngrp) : pick_mt_u<BF16, LAYOUT, ST, ZP, kRing>(mt, ngrp);
 }
 
-DecodeFn pick_decode(int layout, int xtype, int stype, bool zp, int mt, int ngrp) {
-    return xtype == X_BF16 ? pick_layout<true>(layout, stype, zp, mt, ngrp)
-                           : pick_layout<false>(layout, stype, zp, mt, ngrp);
+template <bool BF16>
+DecodeFn pick_layout(int layout, int stype, bool zp, int mt, int ngrp, int ring) {
+    if (layout == LAYOUT_CT) return (zp || stype != S_F32) ? nullptr : pick_mt<BF16, LAYOUT_CT, float, false>(mt, ngrp, ring);
+    if (stype == S_F32) {
+        return zp ? pick_mt<BF16, LAYOUT_MARLIN, float, true>(mt, ngrp, ring)
+                  : pick_mt<BF16, LAYOUT_MARLIN, float, false>(mt, ngrp, ring);
+    }
+    return zp ? pick_mt<BF16, LAYOUT_MARLIN, _Float16, true>(mt, ngrp, ring)
+              : pick_mt<BF16, LAYOUT_MARLIN, _Float16, false>(mt, ngrp, ring);
+}
+
+DecodeFn pick_decode(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring) {
+    return xtype == X_BF16 ? pick_layout<true>(layout, stype, zp, mt, ngrp, ring)
+                           : pick_layout<false>(layout, stype, zp, mt, ngrp, ring);
 }
 
 hipError_t prepare(DecodeFn fn, size_t lds) {
@@ -530,8 +540,8 @@ size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16) {
 
 int decode_threads() { return kThreads; }
 
-int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, size_t lds) {
-    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, mt, ngrp);
+int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, size_t lds) {
+    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, mt, ngrp, ring);
     if (fn == nullptr) return 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
@@ -556,7 +566,7 @@ int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int 
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          int grid_x, hipStream_t stream) {
-    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp);
+    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp, cfg.ring);
     if (fn == nullptr) return hipErrorInvalidValue;
     hipError_t e = prepare(fn, cfg.lds_bytes);
     if (e != hipSuccess) return e;

@@ -53,6 +53,7 @@ struct DecodeConfig {
     int ngrp;    // quant groups per 128-K step (1 when G % 128 == 0, 2 when G == 64)
     int splits;  // K slices
     int k_per_split;
+    int ring;    // weight-load ring depth in steps: 4 or 8
     size_t lds_bytes;
 };
 
@@ -62,7 +63,7 @@ size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16);
 int decode_threads();
 // Resident decode workgroups per CU for the kernel variant and LDS size
 // (0 when the variant does not exist or the runtime cannot tell).
-int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, size_t lds);
+int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, size_t lds);
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          int grid_x, hipStream_t stream);
