@@ -22,7 +22,7 @@ INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(HERE, "_build")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-HIP_SOURCES = ["repack.hip", "gemm_decode.hip", "gemm_prefill.hip", "capi.hip"]
+HIP_SOURCES = ["repack.hip", "gemm_decode.hip", "gemm_prefill.hip", "gemm_prefill_256.hip", "capi.hip"]
 LIB_NAME = "libpulsar_w4a16.so"
 TORCH_LIB_NAME = "_pulsar_w4a16_torch.so"
 

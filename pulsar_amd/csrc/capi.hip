@@ -55,8 +55,17 @@ int decode_nb_override() {
     return (v == 16 || v == 32 || v == 64) ? v : 0;
 }
 
+// Prefill tile override (128 or 256) for tuning sweeps; 0 = heuristic.
+int prefill_tile_override() {
+    const char* e = std::getenv("PW4_PREFILL_TILE");
+    if (!e) return 0;
+    const int v = std::atoi(e);
+    return (v == 128 || v == 256) ? v : 0;
+}
+
 struct Plan {
     bool decode = false;
+    bool p256 = false;       // prefill on the 256 x 256 tile kernel
     DecodeConfig dc{};
     int p_splits = 1;        // prefill K splits
     int p_cps = 0;           // prefill chunks per split
@@ -150,14 +159,24 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
     }
     if (!p.decode) {
         const int64_t nchunks = ceil_div(kext, 64);
-        const int64_t base = ceil_div(M, prefill_tile_m()) * ceil_div(N, prefill_tile_n());
+        // The 256 x 256 kernel (MARLIN, fp16) needs whole 64-K chunks inside one
+        // quant group; measured faster than the 128 x 128 kernel from M = 256 on
+        // every Llama-3-8B layer shape, and used once M passes half its tile.
+        const bool ok256 = prefill256_ok(layout, x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16, N, K, G);
+        const int tile_pref = prefill_tile_override();
+        p.p256 = ok256 && (tile_pref == 256 || (tile_pref == 0 && M > 128));
+        const int64_t tm = p.p256 ? prefill256_tile() : prefill_tile_m();
+        const int64_t tn = p.p256 ? prefill256_tile() : prefill_tile_n();
+        const int64_t base = ceil_div(M, tm) * ceil_div(N, tn);
+        // K slices fill the chip when the tiles do not, but each costs an fp32
+        // partial round trip of the output: keep at least 16 chunks per slice.
         int64_t s;
         if (forced) {
             s = num_splits;
         } else if (base >= cus || nchunks < 8) {
             s = 1;
         } else {
-            s = std::min<int64_t>(ceil_div(cus, std::max<int64_t>(base, 1)), nchunks / 4);
+            s = std::min<int64_t>(ceil_div(cus, std::max<int64_t>(base, 1)), p.p256 ? nchunks / 16 : nchunks / 4);
             s = std::max<int64_t>(s, 1);
         }
         int64_t cps = std::max<int64_t>(ceil_div(std::max<int64_t>(nchunks, 1), s), 1);
@@ -245,7 +264,8 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.nchunks = (int)ceil_div(kext, 64);
         a.chunks_per_split = p.p_cps;
         a.splits = p.p_splits;
-        e = launch_prefill(layout, xt, stype, qzeros != nullptr, a, stream);
+        e = p.p256 ? launch_prefill256(stype, qzeros != nullptr, a, stream)
+                   : launch_prefill(layout, xt, stype, qzeros != nullptr, a, stream);
         if (e != hipSuccess) return hip_fail(e);
     }
     if (p.use_partial && !p.decode) {

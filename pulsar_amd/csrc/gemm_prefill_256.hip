@@ -1,0 +1,332 @@
+// Compute-bound W4A16 GEMM for large M on the MARLIN layout with fp16
+// activations: y[M,N] = x[M,K] @ dequant(W)^T, 256 x 256 output tile per
+// workgroup.
+//
+// Tiling.  Four waves; wave w owns MARLIN column block w of the tile (64
+// columns) for all 256 rows: 8 x 2 tiles of v_mfma_f32_32x32x16_f16 with the
+// fp32 accumulators in AGPRs.  Splitting the tile by columns means every
+// weight nibble is dequantized exactly once per workgroup; the activation
+// tile is read from LDS by all four waves instead.  K advances in 64-wide
+// chunks (one MARLIN chunk per column block).
+//
+// Pipeline.  Three LDS stages of (activations 32 KB, packed weights 8 KB,
+// scales, zero points), filled with global_load_lds (no VGPRs; each lane
+// names its own global address, the 64 lanes of an instruction fill 64
+// consecutive LDS elements).  The copies are issued from inline assembly so
+// that the compiler does not serialise them: it would otherwise wait for
+// every outstanding LDS copy before each LDS read.  The kernel counts them
+// itself instead: every wave issues the same number of copies per chunk, so
+// "chunk i has landed" is vmcnt <= (copies of chunk i+1), then a barrier.
+// Activation rows are XOR-swizzled in 16-byte units (chunk ^ (row & 7)) so
+// the 32 rows an MFMA reads hit distinct LDS banks.
+//
+// Dequant.  Pair p of MARLIN word tg (nibbles p, p+4) holds natural K
+// {8p + 2tg, 8p + 2tg + 1}, so pair p of a column's four words is the K run
+// [8p, 8p + 8) -- exactly what one lane supplies to an MFMA.  Per pair:
+// shift, splice into 1024.0 (exact 1024 + u), subtract 1024 + z (exact), times
+// the group scale (one fp16 rounding, as the reference's dequant_scale,
+// w4a16_marlin.cu:103-113).
+//
+// Reference counterpart: w4a16_marlin_kernel at BM = 64
+// (pulsar-core/src/kernels/w4a16_marlin.cu:197-304).
+#include "w4a16_common.h"
+#include "w4a16_kernels.h"
+
+namespace pw4 {
+namespace {
+
+constexpr int kT = 256;
+constexpr int TM = 256, TN = 256, TK = 64;
+constexpr int kStages = 3;
+constexpr int kAStage = TM * TK * 2;  // bytes
+constexpr int kBStage = TN * TK / 2;
+constexpr int kSStage = 4 * 256;      // per wave 256 bytes of scales (64 fp32, or 64 fp16 + pad)
+constexpr int kZStage = 4 * 256;      // per wave 256 bytes of zero-point words (8 used)
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)p;
+}
+
+// One LDS copy instruction: lane l copies 16 (or 4) bytes from g to
+// LDS[lds + l * 16 (or 4)].  M0 (the LDS base) is saved and restored around
+// it; the s_nop covers the M0-write -> LDS-DMA hazard.
+__device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(lds)
+        : "memory");
+}
+__device__ __forceinline__ void lds_copy4(const void* g, uint32_t lds) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dword %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(lds)
+        : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+template <typename ST, bool ZP, bool PARTIAL>
+__global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
+    __shared__ __attribute__((aligned(16))) uint8_t sA[kStages][kAStage];
+    __shared__ __attribute__((aligned(16))) uint8_t sB[kStages][kBStage];
+    __shared__ __attribute__((aligned(16))) uint8_t sS[kStages][kSStage];
+    __shared__ __attribute__((aligned(16))) uint8_t sZ[kStages][kZStage];
+    // copies per wave per chunk: 8 activation, 2 weight, 1 scale, 1 zero point
+    constexpr int kCopies = 8 + 2 + 1 + (ZP ? 1 : 0);
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int c = lane & 31, hb = lane >> 5;
+    const int M = a.M, N = a.N, K = a.K;
+
+    // ---- tile order: XCD-aware, then grouped along M for L2 reuse ----------
+    const int num_m = (M + TM - 1) / TM, num_n = (N + TN - 1) / TN;
+    const int nwg = num_m * num_n;
+    int pid = blockIdx.x;
+    if ((nwg & 7) == 0) pid = (pid & 7) * (nwg >> 3) + (pid >> 3);  // consecutive tiles share an XCD
+    constexpr int GM = 4;
+    const int group = pid / (GM * num_n);
+    const int first_m = group * GM;
+    const int gsz = min(num_m - first_m, GM);
+    const int in_group = pid - group * GM * num_n;
+    const int m0 = (first_m + in_group % gsz) * TM;
+    const int n0 = (in_group / gsz) * TN;
+
+    const int split = blockIdx.z;
+    const int c_begin = split * a.chunks_per_split;
+    const int c_end = min(c_begin + a.chunks_per_split, a.nchunks);
+    const int nck = max(c_end - c_begin, 0);
+
+    const int ncb = (N + 63) / 64;              // MARLIN column blocks present
+    const int cbw = min(n0 / 64 + wave, ncb - 1);  // this wave's block (clamped: junk columns are never stored)
+    const int ncol0 = n0 + wave * 64;           // first column of this wave
+    const ST* scales = reinterpret_cast<const ST*>(a.scales);
+
+    // ---- copies of one chunk into a stage (unconditional: constant count) ---
+    // Rows past M, columns past N read clamped addresses; their results are
+    // never stored.
+    auto issue = [&](int kc, int st) {
+        const uint32_t abase = lds_addr(&sA[st][0]) + wave * 512 * 16;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int row = wave * 64 + i * 8 + (lane >> 3);
+            const int kch = (lane & 7) ^ (row & 7);
+            const int gm = min(m0 + row, M - 1);
+            lds_copy16(a.x + (int64_t)gm * K + kc * TK + kch * 8, abase + i * 64 * 16);
+        }
+        const uint32_t* wsrc = a.w + ((int64_t)cbw * a.nchunks + kc) * kChunkWords;
+        const uint32_t bbase = lds_addr(&sB[st][0]) + wave * 2048;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) lds_copy16(wsrc + (i * 64 + lane) * 4, bbase + i * 1024);
+        const int g = min(kc * TK / a.G, a.Kg - 1);
+        const uint32_t sbase = lds_addr(&sS[st][0]) + wave * 256;
+        if constexpr (sizeof(ST) == 4) {
+            lds_copy4(scales + (int64_t)g * N + min(ncol0 + lane, N - 1), sbase);
+        } else {
+            lds_copy4(scales + (int64_t)g * N + min(ncol0 + 2 * lane, N - 2), sbase);  // N even
+        }
+        if constexpr (ZP) {
+            const int nw = N / 8;
+            lds_copy4(a.qzeros + (int64_t)g * nw + min(ncol0 / 8 + lane, nw - 1), lds_addr(&sZ[st][0]) + wave * 256);
+        }
+    };
+
+    f32x16 acc[8][2];
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[rt][ct][e] = 0.f;
+
+    // splice constant in a VGPR (the mask comes in an SGPR): one v_and_or_b32
+    uint32_t one;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(one) : "s"(0x64006400u));
+
+    // One chunk = four 16-K steps; step s is pair s % 2 of 32-K tile s / 2, and
+    // this lane's K run in it is [16s + 8hb, +8): activation 16-byte unit
+    // 2s + hb, weight nibble pair 2(s % 2) + hb.  Operands of step s + 1 (eight
+    // A fragments, the dequantized B) are fetched while step s's 16 MFMAs run.
+    auto compute = [&](int st) {
+        const uint8_t* A = &sA[st][0];
+        const uint8_t* B = &sB[st][0] + wave * 2048;
+        u32x4 wq[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) wq[t][ct] = *reinterpret_cast<const u32x4*>(B + t * 1024 + (ct * 32 + c) * 16);
+        f16x2 s2[2], z2[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const int cl = ct * 32 + c;  // column inside the wave's block
+            float sf;
+            if constexpr (sizeof(ST) == 4) {
+                sf = *reinterpret_cast<const float*>(&sS[st][wave * 256 + cl * 4]);
+            } else {
+                sf = (float)*reinterpret_cast<const _Float16*>(&sS[st][wave * 256 + cl * 2]);
+            }
+            const _Float16 sh = (_Float16)sf;
+            s2[ct] = f16x2{sh, sh};
+            uint32_t z = 8u;
+            if constexpr (ZP) z = (*reinterpret_cast<const uint32_t*>(&sZ[st][wave * 256 + (cl >> 3) * 4]) >> (4 * (cl & 7))) & 0xfu;
+            z2[ct] = as_h2((0x6400u | z) * 0x10001u);  // 1024 + z
+        }
+        auto load_a = [&](int s, u32x4 (&av)[8]) {
+            const int kch = 2 * s + hb;
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt) {
+                const int row = rt * 32 + c;
+                av[rt] = *reinterpret_cast<const u32x4*>(A + row * (TK * 2) + ((kch ^ (row & 7)) * 16));
+            }
+        };
+        auto dequant = [&](int s, u32x4 (&bv)[2]) {
+            const int sh = 8 * (s & 1) + 4 * hb;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int tg = 0; tg < 4; ++tg) {
+                    const uint32_t v = ((wq[s >> 1][ct][tg] >> sh) & mk.lo) | one;
+                    bv[ct][tg] = as_u32((as_h2(v) - z2[ct]) * s2[ct]);
+                }
+        };
+        u32x4 av[2][8], bv[2][2];
+        load_a(0, av[0]);
+        dequant(0, bv[0]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int cur = s & 1;
+            if (s < 3) {
+                load_a(s + 1, av[cur ^ 1]);
+                dequant(s + 1, bv[cur ^ 1]);
+            }
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = mfma32x32x16<false>(av[cur][rt], bv[cur][ct], acc[rt][ct]);
+            // interleave: per A fragment of the next step, two MFMAs and its
+            // dequant share
+            if (s < 3) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    if (nck > 0) issue(c_begin, 0);
+    if (nck > 1) issue(c_begin + 1, 1);
+    for (int i = 0; i < nck; ++i) {
+        const int st = i % kStages;
+        if (i + 1 < nck) {
+            wait_vmcnt<kCopies>();  // this wave's copies of chunk i have landed
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads();            // everyone's have; everyone is done with chunk i - 1
+        if (i + 2 < nck) issue(c_begin + i + 2, (i + 2) % kStages);
+        compute(st);
+    }
+
+    // ---- epilogue: D lane holds column c, rows 8*(e/4) + 4*hb + e%4 ---------
+    // Range-checked buffer stores: the resource covers rows [m0, M) of the
+    // output (below 2 GiB), so rows past M are dropped by the hardware; lanes
+    // whose column is past N start at 2 GiB, beyond the range.
+    const int rows = min(M - m0, TM);
+    if constexpr (!PARTIAL) {
+        const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(a.y + (int64_t)m0 * N, (short)0,
+                                                                            rows * N * 2, 0x00020000);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const int n = ncol0 + ct * 32 + c;
+            const uint32_t base = n < N ? (uint32_t)(4 * hb * N + n) * 2u : 0x80000000u;
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int r = rt * 32 + 8 * (e >> 2) + (e & 3);  // row offset without 4 * hb
+                    const uint32_t off = base + (uint32_t)(r * N * 2);
+                    __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<false>(acc[rt][ct][e]), out, (int)off, 0, 0);
+                }
+            // one fragment at a time keeps the converted values few
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    } else {
+        const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+            a.partial + ((int64_t)split * M + m0) * N, (short)0, rows * N * 4, 0x00020000);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const int n = ncol0 + ct * 32 + c;
+            const uint32_t base = n < N ? (uint32_t)(4 * hb * N + n) * 4u : 0x80000000u;
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int r = rt * 32 + 8 * (e >> 2) + (e & 3);
+                    const uint32_t off = base + (uint32_t)(r * N * 4);
+                    // copy out first: bit-casting the vector element itself
+                    // reads element 0 (clang)
+                    const float v = acc[rt][ct][e];
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), out, (int)off, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool prefill256_ok(int layout, int xtype, int64_t N, int64_t K, int64_t G) {
+    // 32-bit buffer offsets: a 256-row fp32 partial tile of the output must
+    // stay below 2 GiB
+    return layout == LAYOUT_MARLIN && xtype == X_F16 && K % TK == 0 && G % TK == 0 && N % 8 == 0 &&
+           N <= (int64_t{1} << 20);
+}
+
+int prefill256_tile() { return TM; }
+
+template <typename ST, bool ZP>
+void launch_variant(const PrefillArgs& a, dim3 grid, hipStream_t stream) {
+    const NibbleMasks mk{};
+    if (a.partial != nullptr) {
+        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, true>), grid, dim3(kT), 0, stream, a, mk);
+    } else {
+        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, false>), grid, dim3(kT), 0, stream, a, mk);
+    }
+}
+
+hipError_t launch_prefill256(int stype, bool zp, const PrefillArgs& a, hipStream_t stream) {
+    const int nwg = (int)(ceil_div(a.M, TM) * ceil_div(a.N, TN));
+    const dim3 grid(nwg, 1, a.splits);
+    if (stype == S_F32) {
+        zp ? launch_variant<float, true>(a, grid, stream) : launch_variant<float, false>(a, grid, stream);
+    } else {
+        zp ? launch_variant<_Float16, true>(a, grid, stream) : launch_variant<_Float16, false>(a, grid, stream);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace pw4

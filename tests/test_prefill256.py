@@ -1,0 +1,79 @@
+"""GPU parity of the 256 x 256 prefill kernel (MARLIN layout, fp16 activations)
+against the fp32 oracle, on ragged M / N, every group size it takes, symmetric
+and asymmetric weights with act-order, and forced K splits.  The tile choice is
+pinned through PW4_PREFILL_TILE so that small cases reach this kernel; the
+same cases on the 128 x 128 kernel must agree with the oracle as well.
+
+Counterpart of the reference's large-M cases, pulsar/tests/test_w4a16_marlin.py:16-208.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from pulsar_amd import ops
+from w4a16_case import baseline_case, check, reference_case
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=[256, 128], ids=["tile256", "tile128"])
+def tile(request):
+    old = os.environ.get("PW4_PREFILL_TILE")
+    os.environ["PW4_PREFILL_TILE"] = str(request.param)
+    yield request.param
+    if old is None:
+        del os.environ["PW4_PREFILL_TILE"]
+    else:
+        os.environ["PW4_PREFILL_TILE"] = old
+
+
+@pytest.mark.parametrize("m,n,k,g", [(65, 64, 64, 64), (300, 200, 320, 64), (257, 520, 1024, 128),
+                                     (512, 4104, 256, 128), (700, 1000, 2048, 64), (1024, 768, 1536, 1536),
+                                     (96, 8, 128, 64)])
+def test_prefill_marlin_ragged(tile, m, n, k, g):
+    c = reference_case(m, n, k, g, torch.float16, seed=11)
+    wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float16), g)
+    y = ops.gemm_w4a16_marlin(c.x, wm, sm, g)
+    check(y, c.y_ref, torch.float16, f"tile={tile} m={m} n={n} k={k} g={g}")
+
+
+@pytest.mark.parametrize("num_splits", [1, 2, 3, 7])
+def test_prefill_marlin_split(tile, num_splits):
+    m, n, k, g = 600, 384, 2048, 128
+    c = reference_case(m, n, k, g, torch.float16, seed=12)
+    wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float16), g)
+    y = ops.gemm_w4a16_marlin_split(c.x, wm, sm, g, num_splits)
+    check(y, c.y_ref, torch.float16, f"tile={tile} split={num_splits}")
+
+
+@pytest.mark.parametrize("sym,act", [(True, False), (False, False), (False, True)])
+@pytest.mark.parametrize("sdtype", [torch.float16, torch.float32])
+def test_prefill_gptq(tile, sym, act, sdtype):
+    m, n, k, g = 520, 328, 1024, 64
+    c = baseline_case(m, n, k, g, seed=13, symmetric=sym, act_order=act)
+    g_idx = torch.from_numpy(c.g_idx).cuda() if act else None
+    wm, perm = ops.repack_w4a16_gptq(c.qweight(), g_idx, g)
+    scales = torch.from_numpy(np.ascontiguousarray(c.scale_nk.T)).to(sdtype).cuda()
+    qz = None if sym else c.qzeros()
+    y = ops.gemm_w4a16_gptq(c.x, wm, scales, qz, perm if act else None, g)
+    check(y, c.y_ref, torch.float16, f"tile={tile} gptq sym={sym} act={act} scales={sdtype}")
+
+
+def test_prefill_tiles_agree():
+    """Both prefill kernels accumulate in fp32 over the same dequantized fp16
+    weights; their outputs agree to fp16 output rounding."""
+    m, n, k, g = 1024, 1024, 2048, 128
+    c = reference_case(m, n, k, g, torch.float16, seed=14)
+    wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float16), g)
+    ys = {}
+    for t in (128, 256):
+        os.environ["PW4_PREFILL_TILE"] = str(t)
+        try:
+            ys[t] = ops.gemm_w4a16_marlin(c.x, wm, sm, g).float()
+        finally:
+            del os.environ["PW4_PREFILL_TILE"]
+    diff = (ys[128] - ys[256]).abs().max().item()
+    assert diff <= 2e-3 * ys[128].abs().max().item(), diff
