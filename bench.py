@@ -25,8 +25,13 @@ reused only after ~850 MB of other weights have streamed through.
 Also reported:
   reference_api = the same sweep through the reference's API
                   (gemm_w4a16_marlin with fp32 scale_marlin from repack_w4a16);
-  prefill       = M = 4096 over the same layers, TFLOP/s
-                  = 2*M*N*K / mean launch time, vs 2516.6 TFLOP/s fp16 MFMA;
+  prefill       = M in {256, 1024, 4096} over the same layers (BASELINE
+                  configs[2]), TFLOP/s = 2*M*N*K / mean launch time, vs
+                  2516.6 TFLOP/s fp16 MFMA;
+  stack         = the 32-layer Llama-3-8B linear stack (q, k, v, o, gate, up,
+                  down per layer) replayed as one HIP graph
+                  per step at M = 1 and M = 32: linear-layer time per decode
+                  step and its HBM GB/s;
   cpu_baseline  = the reference CPU path (dequantize to fp32, fp32 GEMM --
                   the reference test oracle restated in oracle/) on this
                   host's cores over a bounded sample of the sweep.
@@ -50,7 +55,9 @@ FP16_PEAK_TFLOPS = 2516.6
 
 LLAMA8B = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 28672), ("down", 14336, 4096)]
 DECODE_M = [1, 4, 8, 16]
-PREFILL_M = 4096
+PREFILL_M = [256, 1024, 4096]
+STACK_LAYERS = 32
+STACK_M = [1, 32]
 G = 128
 COPIES = 8
 REPS = 4
@@ -160,6 +167,38 @@ def time_graphs(torch, graphs, shapes, steps, warmup, stream):
     return wall, per_shape
 
 
+def stack_bench(torch, dev, steps: int, warmup: int) -> dict:
+    """Config 5: the 32-layer linear stack as one graph per step, M = 1 and 32."""
+    from pulsar_amd.stack import W4A16LinearStack, random_layers
+
+    layers = random_layers(STACK_LAYERS, device=dev, seed=0)
+    out = {"layers": STACK_LAYERS, "linears_per_layer": len(layers[0]),
+           "weight_bytes": sum(l.weight_marlin.numel() * 4 + l.scales.numel() * 2 for ly in layers for l in ly)}
+    for m in STACK_M:
+        st = W4A16LinearStack(layers, m, device=dev)
+        st.capture()
+        for _ in range(warmup):
+            st.step()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        with torch.cuda.stream(st.stream):
+            for a, b in ev:
+                a.record(st.stream)
+                st.step()
+                b.record(st.stream)
+        torch.cuda.synchronize()
+        ms = sorted(a.elapsed_time(b) for a, b in ev)
+        med = ms[len(ms) // 2]
+        gbs = st.bytes_per_step() / (med * 1e-3) / 1e9
+        out[f"m{m}"] = {"us_per_step": round(med * 1e3, 1), "min_us": round(ms[0] * 1e3, 1),
+                        "launches": st.launches_per_step(), "bytes_per_step": st.bytes_per_step(),
+                        "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
+        del st
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,6 +208,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-reference-api", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--no-stack", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the W4A16 path has no multi-GPU component in this build "
@@ -225,23 +265,31 @@ def main() -> int:
     prefill = None
     if not args.no_prefill:
         prefill = {}
-        for name, k, n in LLAMA8B:
-            x = torch.randn(PREFILL_M, k, device=dev).half()
-            w = weights[name][0]
-            for _ in range(2):
-                gemm_fp16_scales(x, w)
-            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(args.prefill_reps)]
-            for i, (a, b) in enumerate(ev):
-                w = weights[name][i % COPIES]
-                a.record()
-                gemm_fp16_scales(x, w)
-                b.record()
-            torch.cuda.synchronize()
-            ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
-            tf = 2.0 * PREFILL_M * n * k / (ms * 1e-3) / 1e12
-            prefill[f"{name}_m{PREFILL_M}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
-                                               "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3)}
+        for pm in PREFILL_M:
+            for name, k, n in LLAMA8B:
+                x = torch.randn(pm, k, device=dev).half()
+                w = weights[name][0]
+                for _ in range(2):
+                    gemm_fp16_scales(x, w)
+                ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                      for _ in range(args.prefill_reps)]
+                for i, (a, b) in enumerate(ev):
+                    w = weights[name][i % COPIES]
+                    a.record()
+                    gemm_fp16_scales(x, w)
+                    b.record()
+                torch.cuda.synchronize()
+                ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+                tf = 2.0 * pm * n * k / (ms * 1e-3) / 1e12
+                prefill[f"{name}_m{pm}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+                                            "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3)}
+                del x
+    del weights, xs
+    torch.cuda.empty_cache()
+
+    stack = None
+    if not args.no_stack:
+        stack = stack_bench(torch, dev, args.steps, args.warmup)
 
     cpu = None if args.no_cpu else cpu_baseline()
     if cpu is not None:
@@ -281,6 +329,7 @@ def main() -> int:
         "decode": per_gemm,
         "reference_api": ref_api,
         "prefill": prefill,
+        "stack": stack,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -107,7 +107,9 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         // slice costs a partial round trip per unit.
         int64_t s = 1;
         if (forced) {
-            s = num_splits;
+            // slices past the last 128-K step would be empty (they add zero):
+            // at most one per step
+            s = std::min<int64_t>(num_splits, steps);
         } else {
             while (s < steps && lds_for(s) > kDecodeLdsLimit) ++s;
         }
@@ -172,7 +174,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         // partial round trip of the output: keep at least 16 chunks per slice.
         int64_t s;
         if (forced) {
-            s = num_splits;
+            s = std::min<int64_t>(num_splits, std::max<int64_t>(nchunks, 1));  // more would be empty slices
         } else if (base >= cus || nchunks < 8) {
             s = 1;
         } else {
@@ -238,8 +240,10 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.splits = p.dc.splits;
         const int64_t ncols = layout == LAYOUT_MARLIN ? round_up(N, kMarlinBN) : round_up(N, 16);
         a.ncg = (int)ceil_div(ncols, p.dc.nb);
-        const int grid_x = p.dc.wps * p.dc.splits;
-        e = launch_decode(layout, xt, stype, qzeros != nullptr, p.dc, a, grid_x, stream);
+        a.ups = (int)ceil_div(a.ncg, p.dc.wps);
+        a.spr_recip = (uint32_t)(((uint64_t{1} << 32) + (uint64_t)(p.dc.k_per_split / 8 + 1) - 1) /
+                                 (uint64_t)(p.dc.k_per_split / 8 + 1));
+        e = launch_decode(layout, xt, stype, qzeros != nullptr, p.dc, a, stream);
         if (e != hipSuccess) return hip_fail(e);
     } else {
         const uint16_t* xin = reinterpret_cast<const uint16_t*>(x);

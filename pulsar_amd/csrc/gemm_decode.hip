@@ -58,6 +58,24 @@ constexpr int kRing = 8;
 // the VGPR write and inserts the wait states an MFMA reading it needs.
 __device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) { return (a & mask) | b; }
 
+// One LDS-DMA copy: lane l copies 16 bytes from g to LDS[lds + 16 l].  Issued
+// from inline assembly with M0 (the LDS base) saved and restored around it and
+// an s_nop for the M0 -> LDS-DMA hazard: through the builtin the compiler would
+// wait for every outstanding vector load (the weight ring included) before
+// the next barrier or LDS read.  The kernel waits for these copies itself.
+__device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(lds)
+        : "memory");
+}
+
 // s_waitcnt vmcnt(n) leaving lgkmcnt / expcnt alone (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -152,19 +170,24 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     const int c = lane & 15, h = lane >> 4;
     const int M = a.M, N = a.N, K = a.K;
     const int nb = a.nb;
-    const int cwn = nb >> 4;       // column waves
-    const int kwn = kWaves / cwn;  // K waves per 16-column strip
-    const int cw = wave % cwn, kw = wave / cwn;
-    const int split = blockIdx.x / a.wps;
-    const int wl = blockIdx.x - split * a.wps;
-    const int n_units = wl < a.ncg ? (a.ncg - wl + a.wps - 1) / a.wps : 0;
+    // No integer divides before the first loads: nb / 16 and 8 / (nb / 16)
+    // are powers of two, the slice is blockIdx.y, and the unit count follows
+    // from ups = ceil(ncg / wps).
+    const int cwn_log2 = __builtin_ctz((unsigned)nb >> 4);  // column waves: 1, 2 or 4
+    const int cwn = 1 << cwn_log2;
+    const int kwn_log2 = 3 - cwn_log2;                      // K waves per 16-column strip
+    const int kwn = 1 << kwn_log2;
+    const int cw = wave & (cwn - 1), kw = wave >> cwn_log2;
+    const int split = blockIdx.y;
+    const int wl = blockIdx.x;
+    const int n_units = wl + (a.ups - 1) * a.wps < a.ncg ? a.ups : a.ups - 1;
     const int rs = a.rowstride;
     const int kb = split * a.k_per_split;
     const int klen = max(min(kb + a.k_per_split, a.ktiles * 32) - kb, 0);  // multiple of 32
     const int nsteps = (klen / 32 + 3) / 4;
     // Steps per unit, the same for every wave; at least one, so that an empty
     // K slice still finishes its units (zero partials) and counts its arrival.
-    const int spu = max((nsteps + kwn - 1) / kwn, 1);
+    const int spu = max((nsteps + kwn - 1) >> kwn_log2, 1);
     const int spu_pad = (spu + U - 1) / U * U;  // positions per unit, a whole number of ring blocks
 
     float* RED = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + x_slots(M, a.k_per_split) * 16);
@@ -184,12 +207,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     const int kvalid = max(min(klen, K - kb), 0);  // halves of real activations in the slice
     const bool gather = a.perm != nullptr;
     if (!gather) {
+        const uint32_t smem_base = (uint32_t)(uintptr_t)smem;
         for (int b = wave; b * 64 < nslots; b += kWaves) {
             const int f = b * 64 + lane;
-            const int row = f / spr, s8 = f - row * spr;
-            if (row < M && s8 * 8 < kvalid) {
-                __builtin_amdgcn_global_load_lds(a.x + (int64_t)row * K + kb + s8 * 8, smem + b * 512, 16, 0, 0);
-            }
+            const int row = (int)__umulhi((uint32_t)f, a.spr_recip);  // f / spr (exact; checked at launch)
+            const int s8 = f - row * spr;
+            if (row < M && s8 * 8 < kvalid) lds_copy16(a.x + (int64_t)row * K + kb + s8 * 8, smem_base + b * 1024);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -399,15 +422,20 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
         const int col0 = cg * nb;
         const int nout = M * nb;
         auto reduced = [&](int i) {
-            const int row = i / nb, col = i - row * nb;
+            const int row = i >> (4 + cwn_log2), col = i & (nb - 1);
             const int cwi = col >> 4, ci = col & 15;
+            // all kwn reads issued before the first add, summed in K-wave order
+            float t[kWaves];
+#pragma unroll
+            for (int k = 0; k < kWaves; ++k) t[k] = k < kwn ? red[((k * cwn + cwi) * MP + row) * 16 + ci] : 0.f;
             float v = 0.f;
-            for (int k = 0; k < kwn; ++k) v += red[((k * cwn + cwi) * MP + row) * 16 + ci];
+#pragma unroll
+            for (int k = 0; k < kWaves; ++k) v += t[k];
             return v;
         };
         if (a.partial == nullptr) {
             for (int i = tid; i < nout; i += kThreads) {
-                const int row = i / nb, n = col0 + (i - row * nb);
+                const int row = i >> (4 + cwn_log2), n = col0 + (i & (nb - 1));
                 const float v = reduced(i);
                 if (n < N) a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
             }
@@ -438,7 +466,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
                 for (int sp = 0; sp < a.splits; ++sp) {
                     v += __hip_atomic_load(base + (int64_t)sp * nout + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
-                const int row = i / nb, n = col0 + (i - row * nb);
+                const int row = i >> (4 + cwn_log2), n = col0 + (i & (nb - 1));
                 if (n < N) a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
             }
             if (tid == 0) __hip_atomic_store(a.counters + cg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -453,16 +481,22 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     for (int u = 0; u < n_units; ++u) {
         for (int jb = 0; jb < spu_pad; jb += U) {
             // this block's refills: the next block of the unit, or the next
-            // unit's first block
+            // unit's first block; none after the workgroup's last block (a
+            // wave cannot retire before its loads return)
             const bool same = jb + U < spu_pad;
             const int tu = same ? u : u + 1, tj = same ? jb + U : 0;
+            if (same || u + 1 < n_units) {
 #pragma unroll
-            for (int i = 0; i < U; ++i) {
-                compute_step(u, jb + i, ring[i]);
-                load_step(tu, tj + i, ring[i]);
-                // keep the refill right behind its step: without the barrier
-                // the scheduler batches all U computes first and drains the ring
-                __builtin_amdgcn_sched_barrier(0);
+                for (int i = 0; i < U; ++i) {
+                    compute_step(u, jb + i, ring[i]);
+                    load_step(tu, tj + i, ring[i]);
+                    // keep the refill right behind its step: without the barrier
+                    // the scheduler batches all U computes first and drains the ring
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < U; ++i) compute_step(u, jb + i, ring[i]);
             }
         }
         finish_unit(u);
@@ -565,12 +599,16 @@ int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int 
 }
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
-                         int grid_x, hipStream_t stream) {
+                         hipStream_t stream) {
     const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp, cfg.ring);
     if (fn == nullptr) return hipErrorInvalidValue;
+    // the kernel maps slots to rows with a multiply-high by spr_recip, exact
+    // while slot * spr < 2^32
+    const uint64_t spr = (uint64_t)a.k_per_split / 8 + 1;
+    if (x_slots(a.M, a.k_per_split) * spr >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
     hipError_t e = prepare(fn, cfg.lds_bytes);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(fn, dim3(grid_x), dim3(kThreads), cfg.lds_bytes, stream, a);
+    hipLaunchKernelGGL(fn, dim3(a.wps, a.splits), dim3(kThreads), cfg.lds_bytes, stream, a);
     return hipGetLastError();
 }
 

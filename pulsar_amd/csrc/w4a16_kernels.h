@@ -11,9 +11,9 @@ enum XType : int { X_F16 = 0, X_BF16 = 1 };
 enum SType : int { S_F32 = 0, S_F16 = 1 };
 
 // Decode GEMM (M <= 64).  The columns are cut into units of nb (16, 32 or
-// 64) and K into `splits` slices; gridDim.x = wps * splits persistent
-// workgroups of 8 waves, workgroup w taking slice w / wps and the units
-// w % wps, w % wps + wps, ...  With more than one slice, each workgroup writes
+// 64) and K into `splits` slices; a grid of wps x splits persistent
+// workgroups of 8 waves, workgroup (w, s) taking slice s and the units
+// w, w + wps, w + 2 wps, ...  With more than one slice, each workgroup writes
 // an fp32 partial tile per unit and the last one to finish a unit sums the
 // partials in slice order and stores y.
 // Nibble masks for the exponent-splice dequant, passed at run time so the
@@ -36,6 +36,8 @@ struct DecodeArgs {
     int nb;                  // columns per unit: 16, 32 or 64
     int ncg;                 // units (column groups) per slice
     int wps;                 // workgroups per slice
+    int ups;                 // units of the busiest workgroup: ceil(ncg / wps)
+    uint32_t spr_recip;      // ceil(2^32 / (k_per_split / 8 + 1)): slot -> row without a divide
     int M, N, K, G, Kg;
     int G_log2;              // log2(G); G is a power of two on this path
     int ktiles;              // 32-wide K tiles present in the weight layout
@@ -66,7 +68,7 @@ int decode_threads();
 int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, size_t lds);
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
-                         int grid_x, hipStream_t stream);
+                         hipStream_t stream);
 hipError_t launch_combine(const float* partial, uint16_t* y, int64_t mn, int splits, int xtype, hipStream_t stream);
 
 // Prefill GEMM (large M): 128 x 128 output tile per workgroup, BK = 64.

@@ -1,0 +1,61 @@
+"""The Llama-3-8B linear stack as one captured graph.
+
+* every replay reproduces the eager launches bit for bit, with the program's
+  own eager work and synchronisations between replays, and follows new input
+  values written between replays;
+* through the graph, linears built from oracle weights match the fp32 oracle
+  (dequantize-then-matmul) at M = 1 and M = 32.
+"""
+
+import pytest
+import torch
+
+from oracle import oracle as O
+from pulsar_amd import ops
+from pulsar_amd.stack import LLAMA3_8B_LINEARS, QuantLinear, W4A16LinearStack, random_layers
+from w4a16_case import check, to_device_x
+
+pytestmark = pytest.mark.gpu
+
+G = 128
+
+
+@pytest.mark.parametrize("m", [1, 32])
+def test_stack_graph_replays_match_eager(m):
+    layers = random_layers(2, device="cuda:0", seed=3)
+    st = W4A16LinearStack(layers, m)
+    st.capture()
+    assert st.launches_per_step() == 14 and len(st.outputs) == 14
+    assert [tuple(o.shape) for o in st.outputs[:7]] == [(m, n) for _, _, n in LLAMA3_8B_LINEARS]
+    for rep in range(3):
+        st.step()
+        torch.cuda.synchronize()
+        want = st.forward()  # eager, same inputs
+        torch.cuda.synchronize()
+        for i, (got, ref) in enumerate(zip(st.outputs, want)):
+            assert torch.equal(got, ref), f"replay {rep}, linear {i}"
+        # new inputs between replays: the graph reads the same buffers
+        for x in st.inputs.values():
+            x.copy_(torch.randn_like(x, dtype=torch.float32).half())
+
+
+@pytest.mark.parametrize("m", [1, 32])
+def test_stack_graph_matches_oracle(m):
+    probs = {k: O.make_problem(m, n, k, G, seed=20 + i) for i, (_, k, n) in enumerate([("k", 4096, 1024),
+                                                                                    ("down", 14336, 4096)])}
+    layer = []
+    for name, (k, p) in zip(("k", "down"), probs.items()):
+        qweight = torch.from_numpy(O.pack_gptq(p.u)).cuda()
+        wm, _ = ops.repack_w4a16_gptq(qweight, None, G)
+        scales = torch.from_numpy(p.scale_kn).half().cuda()  # exact: the values are fp16
+        layer.append(QuantLinear(name, k, p.n, wm, scales))
+    st = W4A16LinearStack([layer], m)
+    for k, p in probs.items():
+        st.inputs[k].copy_(to_device_x(p.x16, torch.float16))
+    st.capture()
+    for _ in range(2):
+        st.step()
+        torch.cuda.synchronize()
+        for (k, p), y in zip(probs.items(), st.outputs):
+            y_ref = O.gemm_f32(p.xf, p.dequant())
+            check(y, y_ref, torch.float16, f"stack m={m} k={k}")
