@@ -12,9 +12,11 @@ back-to-back on the GPU without host launch gaps.  The timed region replays
 the 16 shape graphs per step, each bracketed by HIP events recorded on the
 replay stream.
   value    = algorithmic bytes of every timed launch / wall time of the
-             timed region (GB/s, whole job).
-  roofline = the decode kernel: algorithmic bytes / summed event time of the
-             shape graphs (per-launch mean), vs 8 TB/s HBM3E.
+             timed region (GB/s, whole job, launch gaps included).
+  roofline = the decode kernel: algorithmic bytes / the kernel's own mean
+             duration, from HIP events around single launches on the launch
+             stream (the graph period above adds the ~1-2 us gap between
+             back-to-back launches), vs 8 TB/s HBM3E.
 Algorithmic bytes per GEMM: N*K/2 (int4) + N*(K/G)*2 (fp16 scales) +
 M*K*2 (x) + M*N*2 (y).
 
@@ -167,15 +169,63 @@ def time_graphs(torch, graphs, shapes, steps, warmup, stream):
     return wall, per_shape
 
 
+COPY_BYTES = 512 << 20
+
+
+def summarize_traffic(fetch_csv: str, write_csv: str) -> int:
+    """HBM bytes per decode launch from two rocprofv3 --pmc runs of --pmc-workload.
+
+    FETCH_SIZE and WRITE_SIZE are KiB per dispatch.  Each is scaled by the
+    factor that makes the 512 MiB copy read (write) exactly 512 MiB, then the
+    decode launches are averaged and set against their algorithmic bytes."""
+    import csv
+
+    def per_dispatch(path, counter):
+        rows = {}
+        for r in csv.DictReader(open(path)):
+            if r.get("Counter_Name") != counter:
+                continue
+            key = r["Dispatch_Id"]
+            rows[key] = (r["Kernel_Name"], rows.get(key, ("", 0.0))[1] + float(r["Counter_Value"]))
+        return list(rows.values())
+
+    out = {}
+    for label, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE")):
+        rows = per_dispatch(path, counter)
+        copy = [v for name, v in rows if "copy" in name.lower()]
+        dec = [v for name, v in rows if "decode_kernel" in name]
+        if not copy or not dec:
+            print(f"{path}: no copy or no decode dispatches for {counter}", file=sys.stderr)
+            return 1
+        factor = (COPY_BYTES / 1024.0) / max(copy)
+        out[label] = {"counter": counter, "copy_kib": max(copy), "calibration_factor": round(factor, 4),
+                      "decode_dispatches": len(dec), "decode_mean_kib": sum(dec) / len(dec),
+                      "decode_mean_bytes_calibrated": sum(dec) / len(dec) * 1024.0 * factor}
+    shapes = [(m, name, k, n) for m in DECODE_M for name, k, n in LLAMA8B]
+    alg = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) / len(shapes)
+    traffic = out["fetch"]["decode_mean_bytes_calibrated"] + out["write"]["decode_mean_bytes_calibrated"]
+    res = {"bytes_per_launch": round(traffic), "algorithmic_bytes_per_launch": round(alg),
+           "traffic_over_algorithmic": round(traffic / alg, 4), "launches": "the 16 decode-sweep shapes x "
+           f"{REPS} launches each, fp16 scales", **out}
+    path = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    with open(path, "w") as f:
+        json.dump(res, f, indent=1)
+    print(json.dumps(res))
+    return 0
+
+
 def stack_bench(torch, dev, steps: int, warmup: int) -> dict:
     """Config 5: the 32-layer linear stack as one graph per step, M = 1 and 32."""
-    from pulsar_amd.stack import W4A16LinearStack, random_layers
+    from pulsar_amd.stack import W4A16LinearStack, fuse_layers, random_layers
 
     layers = random_layers(STACK_LAYERS, device=dev, seed=0)
     out = {"layers": STACK_LAYERS, "linears_per_layer": len(layers[0]),
-           "weight_bytes": sum(l.weight_marlin.numel() * 4 + l.scales.numel() * 2 for ly in layers for l in ly)}
-    for m in STACK_M:
-        st = W4A16LinearStack(layers, m, device=dev)
+           "weight_bytes": sum(l.weight_marlin.numel() * 4 + l.scales.numel() * 2 for ly in layers for l in ly),
+           "note": "m1/m32: the 7 linears per layer as 7 launches; fused_m1/fused_m32: q|k|v and gate|up "
+                   "N-concatenated (4 launches per layer, same weights and outputs)"}
+    fused = fuse_layers(layers)
+    for tag, ls, m in [(f"m{m}", layers, m) for m in STACK_M] + [(f"fused_m{m}", fused, m) for m in STACK_M]:
+        st = W4A16LinearStack(ls, m, device=dev)
         st.capture()
         for _ in range(warmup):
             st.step()
@@ -190,12 +240,31 @@ def stack_bench(torch, dev, steps: int, warmup: int) -> dict:
         ms = sorted(a.elapsed_time(b) for a, b in ev)
         med = ms[len(ms) // 2]
         gbs = st.bytes_per_step() / (med * 1e-3) / 1e9
-        out[f"m{m}"] = {"us_per_step": round(med * 1e3, 1), "min_us": round(ms[0] * 1e3, 1),
+        out[tag] = {"us_per_step": round(med * 1e3, 1), "min_us": round(ms[0] * 1e3, 1),
                         "launches": st.launches_per_step(), "bytes_per_step": st.bytes_per_step(),
                         "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
         del st
-    del layers
+    del layers, fused
     torch.cuda.empty_cache()
+    return out
+
+
+def time_each_launch(torch, shapes, weights, xs, fn, stream, reps: int) -> list[float]:
+    """Mean duration (ms) of single launches, each bracketed by HIP events on
+    the launch stream: the kernel's own time without the back-to-back launch
+    gap, comparable with rocprofv3's per-dispatch durations."""
+    out = []
+    with torch.cuda.stream(stream):
+        for mi, (m, name, k, n) in enumerate(shapes):
+            first = (DECODE_M.index(m) % 2) * REPS
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for r, (a, b) in enumerate(ev):
+                w = weights[name][(first + r) % COPIES]
+                a.record(stream)
+                fn(xs[(m, k)], w)
+                b.record(stream)
+            stream.synchronize()
+            out.append(sum(a.elapsed_time(b) for a, b in ev) / reps)
     return out
 
 
@@ -209,7 +278,16 @@ def main() -> int:
     ap.add_argument("--no-reference-api", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=10)
     ap.add_argument("--no-stack", action="store_true")
+    ap.add_argument("--pmc-workload", choices=["decode", "prefill"],
+                    help="no timing: decode = the decode sweep's launches once each, then a 512 MiB copy (the "
+                         "HBM counter calibration), for rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE; prefill = "
+                         "one M=4096 launch per layer, for MFMA counters")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode sweep (headline value null)")
+    ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise the two --pmc-workload counter CSVs into profiles/decode_traffic.json")
     args = ap.parse_args()
+    if args.traffic:
+        return summarize_traffic(*args.traffic)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the W4A16 path has no multi-GPU component in this build "
               "(--gpus must be 1)", file=sys.stderr)
@@ -232,19 +310,43 @@ def main() -> int:
     def gemm_reference_api(x, w):
         return pulsar_amd.ops.gemm_w4a16_marlin(x, w[0], w[1], G)
 
-    graphs = build_graphs(torch, shapes, weights, xs, gemm_fp16_scales, stream)
-    wall, per_ms = time_graphs(torch, graphs, shapes, args.steps, args.warmup, stream)
+    if args.pmc_workload == "prefill":
+        for name, k, n in LLAMA8B:
+            x = torch.randn(PREFILL_M[-1], k, device=dev).half()
+            gemm_fp16_scales(x, weights[name][0])
+        torch.cuda.synchronize()
+        return 0
+    if args.pmc_workload == "decode":
+        with torch.cuda.stream(stream):
+            for m, name, k, n in shapes:
+                for r in range(REPS):
+                    gemm_fp16_scales(xs[(m, k)], weights[name][r % COPIES])
+            src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device=dev)
+            dst = torch.empty_like(src)
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return 0
+
+    value = achieved = wall = mean_launch_us = None
+    per_gemm = {}
     launches = args.steps * REPS
     tot_bytes = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) * launches
-    tot_event_s = sum(per_ms) * 1e-3 * launches
-    per_gemm = {}
-    for (m, name, k, n), ms in zip(shapes, per_ms):
-        gbs = decode_bytes(m, k, n) / (ms * 1e-3) / 1e9
-        per_gemm[f"{name}_m{m}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-                                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
-    value = tot_bytes / wall / 1e9
-    achieved = tot_bytes / tot_event_s / 1e9
-    del graphs
+    if not args.no_decode:
+        graphs = build_graphs(torch, shapes, weights, xs, gemm_fp16_scales, stream)
+        wall, per_ms = time_graphs(torch, graphs, shapes, args.steps, args.warmup, stream)
+        tot_event_s = sum(per_ms) * 1e-3 * launches
+        for (m, name, k, n), ms in zip(shapes, per_ms):
+            gbs = decode_bytes(m, k, n) / (ms * 1e-3) / 1e9
+            per_gemm[f"{name}_m{m}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
+        value = tot_bytes / wall / 1e9
+        del graphs
+        # the roofline: algorithmic bytes over the kernel's own duration
+        each_ms = time_each_launch(torch, shapes, weights, xs, gemm_fp16_scales, stream, args.steps * REPS)
+        for (m, name, k, n), ms in zip(shapes, each_ms):
+            per_gemm[f"{name}_m{m}"]["kernel_us"] = round(ms * 1e3, 2)
+        achieved = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) / (sum(each_ms) * 1e-3) / 1e9
+        mean_launch_us = sum(each_ms) / len(each_ms) * 1e3
 
     ref_api = None
     if not args.no_reference_api:
@@ -297,12 +399,12 @@ def main() -> int:
 
     line = {
         "metric": "W4A16 GEMM HBM GB/s (M<=16) & TFLOP/s (M=4096), % of MI355X roofline",
-        "value": round(value, 2),
+        "value": None if value is None else round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "ms_per_step": None if wall is None else round(wall / args.steps * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -320,11 +422,12 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(achieved, 1),
+            "achieved": None if achieved is None else round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "frac": None if achieved is None else round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "mean_launch_us": None if mean_launch_us is None else round(mean_launch_us, 3),
         },
         "decode": per_gemm,
         "reference_api": ref_api,

@@ -41,6 +41,11 @@ LLAMA3_8B_LINEARS = (
 )
 
 
+# The same layer with q|k|v and gate|up each fused into one N-concatenated
+# linear (the decode-sweep shapes qkv 4096x6144 and gate_up 4096x28672).
+LLAMA3_8B_FUSED = (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",)))
+
+
 @dataclass
 class QuantLinear:
     """One linear in the MARLIN layout: weight_marlin int32 words, fp16 scales [K/G, N]."""
@@ -74,6 +79,27 @@ def random_layers(num_layers: int, shapes=LLAMA3_8B_LINEARS, group_size: int = 1
             layer.append(QuantLinear(name, k, n, wm, scales))
         layers.append(layer)
     return layers
+
+
+def fuse_layers(layers: list[list[QuantLinear]], groups=LLAMA3_8B_FUSED) -> list[list[QuantLinear]]:
+    """N-concatenate linears that share their input.  The MARLIN word order is
+    column-block major (64-column blocks, each holding all of K), so for
+    members whose N is a multiple of 64 the fused weight is the members'
+    weight buffers back to back; the scales concatenate along N."""
+    fused = []
+    for layer in layers:
+        by_name = {lin.name: lin for lin in layer}
+        out = []
+        for name, members in groups:
+            parts = [by_name[m] for m in members]
+            k = parts[0].k
+            if any(p.k != k for p in parts) or any(p.n % 64 for p in parts[:-1]):
+                raise ValueError(f"cannot fuse {members}: K differs or N not a multiple of 64")
+            wm = torch.cat([p.weight_marlin for p in parts]) if len(parts) > 1 else parts[0].weight_marlin
+            sc = torch.cat([p.scales for p in parts], dim=1) if len(parts) > 1 else parts[0].scales
+            out.append(QuantLinear(name, k, sum(p.n for p in parts), wm, sc))
+        fused.append(out)
+    return fused
 
 
 class W4A16LinearStack:

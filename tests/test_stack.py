@@ -12,7 +12,7 @@ import torch
 
 from oracle import oracle as O
 from pulsar_amd import ops
-from pulsar_amd.stack import LLAMA3_8B_LINEARS, QuantLinear, W4A16LinearStack, random_layers
+from pulsar_amd.stack import LLAMA3_8B_LINEARS, QuantLinear, W4A16LinearStack, fuse_layers, random_layers
 from w4a16_case import check, to_device_x
 
 pytestmark = pytest.mark.gpu
@@ -59,3 +59,27 @@ def test_stack_graph_matches_oracle(m):
         for (k, p), y in zip(probs.items(), st.outputs):
             y_ref = O.gemm_f32(p.xf, p.dequant())
             check(y, y_ref, torch.float16, f"stack m={m} k={k}")
+
+
+@pytest.mark.parametrize("m", [1, 32])
+def test_fused_stack_equals_unfused(m):
+    """q|k|v and gate|up fused along N compute every column exactly as the
+    separate linears do (same K, same per-column reduction)."""
+    layers = random_layers(1, device="cuda:0", seed=5)
+    fused = fuse_layers(layers)
+    assert [(l.name, l.k, l.n) for l in fused[0]] == [("qkv", 4096, 6144), ("o", 4096, 4096),
+                                                      ("gate_up", 4096, 28672), ("down", 14336, 4096)]
+    a = W4A16LinearStack(layers, m, seed=7)
+    b = W4A16LinearStack(fused, m, seed=7)
+    for k in a.inputs:
+        assert torch.equal(a.inputs[k], b.inputs[k])
+    a.capture()
+    b.capture()
+    a.step()
+    b.step()
+    torch.cuda.synchronize()
+    ya, yb = a.outputs, b.outputs
+    torch.testing.assert_close(yb[0], torch.cat(ya[0:3], dim=1), rtol=0, atol=0)
+    torch.testing.assert_close(yb[1], ya[3], rtol=0, atol=0)
+    torch.testing.assert_close(yb[2], torch.cat(ya[4:6], dim=1), rtol=0, atol=0)
+    torch.testing.assert_close(yb[3], ya[6], rtol=0, atol=0)
