@@ -9,12 +9,13 @@
  * (workspace, workspace_bytes) and sized with the matching *_workspace_size
  * query, so the GEMMs are safe under HIP graph capture.
  *
- * Workspace contract.  A non-empty workspace begins with a counter region of
- * PW4_COUNTER_REGION_BYTES that must be zero when the workspace is first
- * used (clear it once after allocating); every GEMM call leaves it zero when
- * it completes, so the workspace can be reused by later calls without
- * clearing.  Calls that share a workspace must be ordered (one stream, or
- * explicit synchronisation); concurrent calls need distinct workspaces.
+ * Workspace contract.  A non-empty workspace begins with a region of
+ * PW4_ZERO_REGION_BYTES (K-split arrival counters and exchange slots) that
+ * must be zero when the workspace is first used (clear it once after
+ * allocating); every GEMM call leaves it zero when it completes, so the
+ * workspace can be reused by later calls without clearing.  The bytes after
+ * it are scratch.  Calls that share a workspace must be ordered (one stream,
+ * or explicit synchronisation); concurrent calls need distinct workspaces.
  *
  * Each entry point replaces one operator of the reference pulsar-core C++ API
  * (pulsar-core/inc/pulsar/ops.hpp) and keeps its argument meaning and its
@@ -42,8 +43,9 @@ typedef struct ihipStream_t* pw4_stream_t; /* == hipStream_t */
 #define PW4_ERR_GIDX (-5)      /* act-order g_idx is not a valid grouping */
 
 /* bytes at the start of every non-empty GEMM workspace that hold the K-split
- * arrival counters (zero before first use, left zero by every call) */
-#define PW4_COUNTER_REGION_BYTES 65536
+ * arrival counters and exchange slots (zero before first use, left zero by
+ * every call) */
+#define PW4_ZERO_REGION_BYTES (16u << 20)
 
 /* element types */
 #define PW4_DTYPE_F16 0
@@ -56,7 +58,7 @@ const char* pw4_status_string(int status);
 const char* pw4_last_hip_error(void);
 /* ABI version of this header: bumped on any incompatible change. */
 int pw4_abi_version(void);
-#define PW4_ABI_VERSION 1
+#define PW4_ABI_VERSION 2
 
 /* Number of int32 words of the MARLIN layout for an [N, K] weight:
  * roundup(N, 64) * roundup(K, 64) / 8.

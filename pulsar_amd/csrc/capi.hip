@@ -44,8 +44,11 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 constexpr size_t kDecodeLdsLimit = 152 * 1024;
 constexpr size_t kLdsPerCu = 160 * 1024;
 // Arrival counters of the decode K split: one int32 per workgroup column.
-constexpr size_t kCounterRegion = PW4_COUNTER_REGION_BYTES;
-constexpr int64_t kMaxCounterCols = (int64_t)(kCounterRegion / sizeof(int32_t));
+// Zero region of a workspace: arrival counters, then exchange-tree slots.
+constexpr size_t kZeroRegion = PW4_ZERO_REGION_BYTES;
+constexpr size_t kCounterBytes = 65536;
+constexpr int64_t kMaxCounterCols = (int64_t)(kCounterBytes / sizeof(int32_t));
+constexpr size_t kSlotBytes = kZeroRegion - kCounterBytes;
 
 // Decode column width override (16, 32 or 64) for tuning sweeps; 0 = heuristic.
 int decode_nb_override() {
@@ -63,8 +66,18 @@ int prefill_tile_override() {
     return (v == 128 || v == 256) ? v : 0;
 }
 
+// Decode K-split override for tuning sweeps (2, 4 or 8: exchange-tree
+// slices even where the activations fit in LDS); 0 = heuristic.
+int decode_splits_override() {
+    const char* e = std::getenv("PW4_DECODE_SPLITS");
+    if (!e) return 0;
+    const int v = std::atoi(e);
+    return (v == 2 || v == 4 || v == 8) ? v : 0;
+}
+
 struct Plan {
     bool decode = false;
+    bool tree = false;       // decode K slices reduced through the exchange tree
     bool p256 = false;       // prefill on the 256 x 256 tile kernel
     DecodeConfig dc{};
     int p_splits = 1;        // prefill K splits
@@ -73,12 +86,12 @@ struct Plan {
     int splits = 1;
     size_t partial_bytes = 0;
     size_t xperm_bytes = 0;
-    // Every non-empty workspace starts with the fixed counter region, so the
-    // bytes a decode call uses as arrival counters are never scratch for
-    // another call that shares the workspace.
+    // Every non-empty workspace starts with the fixed zero region, so the
+    // bytes a decode call uses as counters or exchange slots are never
+    // scratch for another call that shares the workspace.
     size_t workspace() const {
         const size_t rest = align_up(partial_bytes) + align_up(xperm_bytes);
-        return rest ? kCounterRegion + rest : 0;
+        return (rest || tree) ? kZeroRegion + rest : 0;
     }
 };
 
@@ -102,9 +115,13 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         const int64_t ncols = layout == LAYOUT_MARLIN ? round_up(N, kMarlinBN) : round_up(N, 16);
         const int64_t steps = std::max<int64_t>(ceil_div(ktiles * 32, 128), 1);
         auto kps_for = [&](int64_t sp) { return std::max<int64_t>(round_up(ceil_div(ktiles * 32, sp), 128), 128); };
-        auto lds_for = [&](int64_t sp) { return decode_lds_bytes((int)M, (int)kps_for(sp), dc.ngrp, zp_any, bf); };
+        bool red_single = false;
+        auto lds_for = [&](int64_t sp) {
+            return decode_lds_bytes((int)M, (int)kps_for(sp), dc.ngrp, zp_any, bf, red_single);
+        };
         // K slices only when the activation slice does not fit in LDS: each
-        // slice costs a partial round trip per unit.
+        // slice costs a partial round trip per unit.  A single reduction
+        // buffer is used when it saves slices.
         int64_t s = 1;
         if (forced) {
             // slices past the last 128-K step would be empty (they add zero):
@@ -112,13 +129,39 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
             s = std::min<int64_t>(num_splits, steps);
         } else {
             while (s < steps && lds_for(s) > kDecodeLdsLimit) ++s;
+            if (s > 1) {
+                red_single = true;
+                int64_t s1 = 1;
+                while (s1 < steps && lds_for(s1) > kDecodeLdsLimit) ++s1;
+                if (s1 < s) {
+                    s = s1;
+                } else {
+                    red_single = false;
+                }
+            }
+        }
+        // Exchange-tree slices (no partial round trip, no ring drain): a power
+        // of two up to 8 over 16-column units, one output element per thread.
+        bool tree = false;
+        if (!forced) {
+            int64_t s2 = std::max<int64_t>(s, decode_splits_override());
+            if (s2 > 1) {
+                int64_t p2 = 2;
+                while (p2 < s2) p2 *= 2;
+                const int64_t ncg16 = ceil_div(ncols, 16);
+                if (p2 <= 8 && p2 <= steps && M * 16 <= 512 &&
+                    (size_t)(p2 - 1) * ncg16 * M * 16 * sizeof(uint64_t) <= kSlotBytes) {
+                    s = p2;
+                    tree = true;
+                }
+            }
         }
         const int64_t kps = kps_for(s);
-        if (!forced) s = std::max<int64_t>(ceil_div(ktiles * 32, kps), 1);
+        if (!forced && !tree) s = std::max<int64_t>(ceil_div(ktiles * 32, kps), 1);
         const size_t lds = lds_for(s);
         // Units: 16 columns (eight K waves per strip, the finest balance), or
         // 64 when K is sliced, to keep the per-unit partial round trips few.
-        int nb = decode_nb_override();
+        int nb = tree ? 16 : decode_nb_override();
         if (nb == 0) nb = s > 1 ? 64 : 16;
         while (nb > 16 && ncols % nb != 0) nb /= 2;
         const int64_t ncg = ceil_div(ncols, nb);
@@ -131,7 +174,9 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         // budget), then as few units per workgroup as possible with the
         // least per-CU load.
         int64_t per_cu_max =
-            lds <= kDecodeLdsLimit ? decode_blocks_per_cu(layout, bf ? X_BF16 : X_F16, stype, zp, dc.mt, dc.ngrp, dc.ring, lds) : 0;
+            lds <= kDecodeLdsLimit
+                ? decode_blocks_per_cu(layout, bf ? X_BF16 : X_F16, stype, zp, dc.mt, dc.ngrp, dc.ring, tree, lds)
+                : 0;
         if (per_cu_max <= 0) per_cu_max = std::max<int64_t>(std::min<int64_t>(2, (int64_t)(kLdsPerCu / std::max<size_t>(lds, 1))), 1);
         per_cu_max = std::min<int64_t>(per_cu_max, 2);
         int64_t best_wps = 1, best_cost = INT64_MAX;
@@ -150,9 +195,13 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         dc.k_per_split = (int)kps;
         dc.splits = (int)s;
         dc.lds_bytes = lds;
-        const bool partial = forced || s > 1;
-        if (lds <= kDecodeLdsLimit && !(partial && ncg > kMaxCounterCols) && best_wps * s <= INT32_MAX) {
+        dc.red_single = red_single;
+        dc.tree = tree;
+        const bool partial = !tree && (forced || s > 1);
+        if (lds <= kDecodeLdsLimit && !(partial && ncg > kMaxCounterCols) && best_wps * s <= INT32_MAX &&
+            s <= 65535) {
             p.decode = true;
+            p.tree = tree;
             p.dc = dc;
             p.splits = (int)s;
             p.use_partial = partial;
@@ -209,9 +258,10 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
     if (p.workspace() > 0 && (workspace == nullptr || ws_bytes < p.workspace())) return PW4_ERR_WORKSPACE;
     char* ws = reinterpret_cast<char*>(workspace);
     int32_t* counters = p.workspace() ? reinterpret_cast<int32_t*>(ws) : nullptr;
-    float* partial = p.partial_bytes ? reinterpret_cast<float*>(ws + kCounterRegion) : nullptr;
+    unsigned long long* slots = p.tree ? reinterpret_cast<unsigned long long*>(ws + kCounterBytes) : nullptr;
+    float* partial = p.partial_bytes ? reinterpret_cast<float*>(ws + kZeroRegion) : nullptr;
     uint16_t* xperm =
-        p.xperm_bytes ? reinterpret_cast<uint16_t*>(ws + kCounterRegion + align_up(p.partial_bytes)) : nullptr;
+        p.xperm_bytes ? reinterpret_cast<uint16_t*>(ws + kZeroRegion + align_up(p.partial_bytes)) : nullptr;
     const int xt = x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16;
     const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
     hipError_t e;
@@ -225,6 +275,9 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.y = reinterpret_cast<uint16_t*>(y);
         a.partial = p.use_partial ? partial : nullptr;
         a.counters = counters;
+        a.slots = slots;
+        a.tree_levels = p.tree ? __builtin_ctz((unsigned)p.dc.splits) : 0;
+        a.red_single = p.dc.red_single ? 1 : 0;
         a.nb = p.dc.nb;
         a.wps = p.dc.wps;
         a.M = (int)M;

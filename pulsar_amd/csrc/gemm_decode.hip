@@ -151,9 +151,16 @@ __device__ __forceinline__ float half_to_f32(uint16_t v) {
 //   CP,CQ [steps][NGRP][MT*16] fp32: bf16 only, per-step correction terms
 __host__ __device__ inline size_t x_slots(int M, int kps) { return ((size_t)M * (kps / 8 + 1) + 63) / 64 * 64; }
 __host__ __device__ inline size_t red_floats(int mt) { return (size_t)2 * kWaves * mt * 16 * 16; }
+
+// s_waitcnt lgkmcnt(0); s_barrier: a workgroup barrier over LDS traffic only.
+// __syncthreads() is a workgroup release fence plus the barrier, and once
+// global atomics are in flight that fence waits for every outstanding vector
+// memory operation, the weight ring included.  The memory clobber keeps the
+// compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __host__ __device__ inline size_t corr_floats(int kps, int ngrp, int mt) { return (size_t)(kps / 128) * ngrp * mt * 16; }
 
-template <bool BF16, int LAYOUT, typename ST, int MT, int NGRP, bool ZP, int U>
+template <bool BF16, int LAYOUT, typename ST, int MT, int NGRP, bool ZP, int U, bool TREE>
 __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     __shared__ int s_last;
@@ -191,7 +198,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     const int spu_pad = (spu + U - 1) / U * U;  // positions per unit, a whole number of ring blocks
 
     float* RED = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + x_slots(M, a.k_per_split) * 16);
-    float* CP = RED + red_floats(MT);
+    float* CP = RED + (a.red_single ? red_floats(MT) / 2 : red_floats(MT));
     float* CQ = CP + corr_floats(a.k_per_split, NGRP, MT);
     const ST* scales = reinterpret_cast<const ST*>(a.scales);
 
@@ -266,9 +273,15 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
         }
     };
 
+    // Issue the ring in the refills' order (weights, scale per step): the
+    // loop body's vmcnt waits must hold for its first block too, and loads
+    // grouped by kind here would make every block wait for half the ring.
     Step ring[U];
 #pragma unroll
-    for (int i = 0; i < U; ++i) load_step(0, i, ring[i]);
+    for (int i = 0; i < U; ++i) {
+        load_step(0, i, ring[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     // ---- finish the slice: act-order gather, zero fill, (bf16) corrections --
     if (gather) {
@@ -406,18 +419,81 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
                 for (int r = 0; r < 4; ++r) acc[mt][r] += load_scale(&in.s[gi]) * tmp[gi][mt][r];
     };
 
+    // ---- K slices through a pairwise exchange tree ---------------------------
+    // splits = 2^levels, one output element per thread (M * nb <= 512).  At
+    // level l the slices pair up as subtrees of 2^l: each side swaps its sum
+    // for the 64-bit slot's previous content {value, flag}; the side that
+    // finds its partner's value adds it (a + b == b + a in fp32, so the sum
+    // does not depend on who came first), clears the slot and goes up a
+    // level; after the top level it stores y.  Value and flag travel in one
+    // atomic, so nothing else needs ordering.  A swap's answer is read one
+    // unit later: by then only weight loads issued after it are outstanding,
+    // and in-order vmcnt lets the wave wait for the swap alone instead of
+    // draining the ring.
+    constexpr int kMaxLevels = 3;
+    const int levels = a.tree_levels;
+    uint64_t t_old[kMaxLevels + 1];
+    float t_v[kMaxLevels + 1];
+    bool t_alive[kMaxLevels + 1];
+    int t_cg[kMaxLevels + 1];  // unit of the stage (wave-uniform), -1 when empty
+#pragma unroll
+    for (int k = 0; k <= kMaxLevels; ++k) {
+        t_old[k] = 0;
+        t_v[k] = 0.f;
+        t_alive[k] = false;
+        t_cg[k] = -1;
+    }
+    auto slot = [&](int level, int cg) {
+        const int node = (a.splits - (a.splits >> level)) + (split >> (level + 1));
+        return a.slots + (((int64_t)node * a.ncg + cg) * (M * nb) + tid);
+    };
+    auto swap_in = [&](int level, int cg, float v) -> uint64_t {
+        const unsigned long long mine = (unsigned long long)__builtin_bit_cast(uint32_t, v) | (1ull << 32);
+        return __hip_atomic_exchange(slot(level, cg), mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    auto tree_advance = [&]() {
+#pragma unroll
+        for (int k = kMaxLevels - 1; k >= 0; --k) {
+            if (k >= levels || t_cg[k] < 0) continue;
+            const int cg = t_cg[k];
+            t_cg[k] = -1;
+            bool go = false;
+            float v = 0.f;
+            if (t_alive[k]) {
+                if ((t_old[k] >> 32) != 0) {  // the partner was first: combine, clear the slot
+                    v = __builtin_bit_cast(float, (uint32_t)t_old[k]) + t_v[k];
+                    __hip_atomic_store(slot(k, cg), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    go = true;
+                }
+                t_alive[k] = false;
+            }
+            if (k + 1 < levels) {  // stage k + 1 was emptied earlier in this loop
+                t_cg[k + 1] = cg;
+                t_alive[k + 1] = go;
+                t_v[k + 1] = v;
+                if (go) t_old[k + 1] = swap_in(k + 1, cg, v);
+            } else if (go) {
+                const int row = tid >> (4 + cwn_log2), n = cg * nb + (tid & (nb - 1));
+                if (n < N) a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
+            }
+        }
+    };
+
     // ---- end of a unit: sum the K waves in fixed order, store ----------------
     int rbuf = 0;
     auto finish_unit = [&](int u) {
+        // one RED buffer (LDS-tight plans): wait until the previous unit's
+        // reduction has read it; two: alternate
+        if (a.red_single) lds_barrier();
         float* red = RED + rbuf * (red_floats(MT) / 2);
-        rbuf ^= 1;
+        if (!a.red_single) rbuf ^= 1;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) red[(wave * MP + mt * 16 + 4 * h + r) * 16 + c] = acc[mt][r];
             acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
-        __syncthreads();
+        lds_barrier();
         const int cg = wl + u * a.wps;
         const int col0 = cg * nb;
         const int nout = M * nb;
@@ -433,6 +509,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
             for (int k = 0; k < kWaves; ++k) v += t[k];
             return v;
         };
+        if constexpr (TREE) {
+            tree_advance();
+            const bool mine = tid < nout;
+            const float v = mine ? reduced(tid) : 0.f;
+            t_cg[0] = cg;
+            t_v[0] = v;
+            t_alive[0] = mine;
+            if (mine) t_old[0] = swap_in(0, cg, v);
+            return;
+        }
         if (a.partial == nullptr) {
             for (int i = tid; i < nout; i += kThreads) {
                 const int row = i >> (4 + cwn_log2), n = col0 + (i & (nb - 1));
@@ -478,61 +564,78 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     // and the ring slots stay compile-time.  Refills are unconditional
     // (clamped past the end) so the ring registers are written by the loads
     // themselves, never through a branch join that would force a wait.
+    // Every block refills the ring (the unit's next block, or the next unit's
+    // first) except the workgroup's very last block, which is peeled out of
+    // the loop: a wave cannot retire before its loads return, and a refill
+    // branch inside the loop would merge two ring states at its head, which
+    // makes the compiler's vmcnt waits wait for half the ring.
+    const int nblk = spu_pad / U;
     for (int u = 0; u < n_units; ++u) {
-        for (int jb = 0; jb < spu_pad; jb += U) {
-            // this block's refills: the next block of the unit, or the next
-            // unit's first block; none after the workgroup's last block (a
-            // wave cannot retire before its loads return)
-            const bool same = jb + U < spu_pad;
+        const int refill_blocks = u + 1 < n_units ? nblk : nblk - 1;
+        for (int b = 0; b < refill_blocks; ++b) {
+            const int jb = b * U;
+            const bool same = b + 1 < nblk;
             const int tu = same ? u : u + 1, tj = same ? jb + U : 0;
-            if (same || u + 1 < n_units) {
 #pragma unroll
-                for (int i = 0; i < U; ++i) {
-                    compute_step(u, jb + i, ring[i]);
-                    load_step(tu, tj + i, ring[i]);
-                    // keep the refill right behind its step: without the barrier
-                    // the scheduler batches all U computes first and drains the ring
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < U; ++i) compute_step(u, jb + i, ring[i]);
+            for (int i = 0; i < U; ++i) {
+                compute_step(u, jb + i, ring[i]);
+                load_step(tu, tj + i, ring[i]);
+                // keep the refill right behind its step: without the barrier
+                // the scheduler batches all U computes first and drains the ring
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
+        if (refill_blocks < nblk) {
+#pragma unroll
+            for (int i = 0; i < U; ++i) compute_step(u, (nblk - 1) * U + i, ring[i]);
+        }
         finish_unit(u);
+    }
+    if constexpr (TREE) {
+        // the last units' exchanges: one level per round trip
+#pragma unroll
+        for (int r = 0; r < kMaxLevels; ++r) tree_advance();
     }
 }
 
 using DecodeFn = void (*)(const DecodeArgs);
 
+// The exchange tree is a separate instantiation (MT 1 and 2 only: it needs
+// M * 16 <= 512): its atomics in the unit loop make the compiler's wait
+// counts for the weight ring more conservative, which the plain variants
+// should not pay for.
 template <bool BF16, int LAYOUT, typename ST, bool ZP, int U>
-DecodeFn pick_mt_u(int mt, int ngrp) {
-    if (mt == 1) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 1, 1, ZP, U> : decode_kernel<BF16, LAYOUT, ST, 1, 2, ZP, U>;
-    if (mt == 2) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 2, 1, ZP, U> : decode_kernel<BF16, LAYOUT, ST, 2, 2, ZP, U>;
-    if (mt == 4) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 4, 1, ZP, U> : decode_kernel<BF16, LAYOUT, ST, 4, 2, ZP, U>;
+DecodeFn pick_mt_u(int mt, int ngrp, bool tree) {
+    if (tree) {
+        if (mt == 1) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 1, 1, ZP, U, true> : decode_kernel<BF16, LAYOUT, ST, 1, 2, ZP, U, true>;
+        if (mt == 2) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 2, 1, ZP, U, true> : decode_kernel<BF16, LAYOUT, ST, 2, 2, ZP, U, true>;
+        return nullptr;
+    }
+    if (mt == 1) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 1, 1, ZP, U, false> : decode_kernel<BF16, LAYOUT, ST, 1, 2, ZP, U, false>;
+    if (mt == 2) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 2, 1, ZP, U, false> : decode_kernel<BF16, LAYOUT, ST, 2, 2, ZP, U, false>;
+    if (mt == 4) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 4, 1, ZP, U, false> : decode_kernel<BF16, LAYOUT, ST, 4, 2, ZP, U, false>;
     return nullptr;
 }
 
-// ring depth: 4 steps when a unit has at most 4 per wave (no padding), else 8
 template <bool BF16, int LAYOUT, typename ST, bool ZP>
-DecodeFn pick_mt(int mt, int ngrp, int ring) {
-    return ring == 4 ? pick_mt_u<BF16, LAYOUT, ST, ZP, 4>(mt, ngrp) : pick_mt_u<BF16, LAYOUT, ST, ZP, kRing>(mt, ngrp);
+DecodeFn pick_mt(int mt, int ngrp, int ring, bool tree) {
+    return ring == 4 ? pick_mt_u<BF16, LAYOUT, ST, ZP, 4>(mt, ngrp, tree) : pick_mt_u<BF16, LAYOUT, ST, ZP, kRing>(mt, ngrp, tree);
 }
 
 template <bool BF16>
-DecodeFn pick_layout(int layout, int stype, bool zp, int mt, int ngrp, int ring) {
-    if (layout == LAYOUT_CT) return (zp || stype != S_F32) ? nullptr : pick_mt<BF16, LAYOUT_CT, float, false>(mt, ngrp, ring);
+DecodeFn pick_layout(int layout, int stype, bool zp, int mt, int ngrp, int ring, bool tree) {
+    if (layout == LAYOUT_CT) return (zp || stype != S_F32) ? nullptr : pick_mt<BF16, LAYOUT_CT, float, false>(mt, ngrp, ring, tree);
     if (stype == S_F32) {
-        return zp ? pick_mt<BF16, LAYOUT_MARLIN, float, true>(mt, ngrp, ring)
-                  : pick_mt<BF16, LAYOUT_MARLIN, float, false>(mt, ngrp, ring);
+        return zp ? pick_mt<BF16, LAYOUT_MARLIN, float, true>(mt, ngrp, ring, tree)
+                  : pick_mt<BF16, LAYOUT_MARLIN, float, false>(mt, ngrp, ring, tree);
     }
-    return zp ? pick_mt<BF16, LAYOUT_MARLIN, _Float16, true>(mt, ngrp, ring)
-              : pick_mt<BF16, LAYOUT_MARLIN, _Float16, false>(mt, ngrp, ring);
+    return zp ? pick_mt<BF16, LAYOUT_MARLIN, _Float16, true>(mt, ngrp, ring, tree)
+              : pick_mt<BF16, LAYOUT_MARLIN, _Float16, false>(mt, ngrp, ring, tree);
 }
 
-DecodeFn pick_decode(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring) {
-    return xtype == X_BF16 ? pick_layout<true>(layout, stype, zp, mt, ngrp, ring)
-                           : pick_layout<false>(layout, stype, zp, mt, ngrp, ring);
+DecodeFn pick_decode(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree) {
+    return xtype == X_BF16 ? pick_layout<true>(layout, stype, zp, mt, ngrp, ring, tree)
+                           : pick_layout<false>(layout, stype, zp, mt, ngrp, ring, tree);
 }
 
 hipError_t prepare(DecodeFn fn, size_t lds) {
@@ -565,17 +668,18 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 
 }  // namespace
 
-size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16) {
+size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single) {
     const int mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-    size_t b = x_slots(M, kps) * 16 + red_floats(mt) * 4;
+    size_t b = x_slots(M, kps) * 16 + red_floats(mt) * 4 / (red_single ? 2 : 1);
     if (bf16) b += corr_floats(kps, ngrp, mt) * 4 * (zp ? 2 : 1);
     return b;
 }
 
 int decode_threads() { return kThreads; }
 
-int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, size_t lds) {
-    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, mt, ngrp, ring);
+int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree,
+                         size_t lds) {
+    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, mt, ngrp, ring, tree);
     if (fn == nullptr) return 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
@@ -600,7 +704,7 @@ int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int 
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          hipStream_t stream) {
-    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp, cfg.ring);
+    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp, cfg.ring, cfg.tree);
     if (fn == nullptr) return hipErrorInvalidValue;
     // the kernel maps slots to rows with a multiply-high by spr_recip, exact
     // while slot * spr < 2^32

@@ -33,6 +33,10 @@ struct DecodeArgs {
     uint16_t* y;             // [M, N] output
     float* partial;          // [ncg, splits, M, nb] fp32, or null for the direct store
     int32_t* counters;       // [ncg] arrival counters (zero on entry, left zero)
+    unsigned long long* slots;  // exchange tree [splits - 1][ncg][M * nb] (zero on entry, left
+                                // zero), or null; used instead of partial/counters
+    int tree_levels;         // log2(splits) with the exchange tree
+    int red_single;          // one cross-wave reduction buffer (see decode_lds_bytes)
     int nb;                  // columns per unit: 16, 32 or 64
     int ncg;                 // units (column groups) per slice
     int wps;                 // workgroups per slice
@@ -56,16 +60,21 @@ struct DecodeConfig {
     int splits;  // K slices
     int k_per_split;
     int ring;    // weight-load ring depth in steps: 4 or 8
+    bool red_single;
+    bool tree;   // K slices through the exchange tree (splits a power of two, M <= 32)
     size_t lds_bytes;
 };
 
 // LDS bytes of one decode workgroup for an M x kps activation slice, and its
 // thread count.
-size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16);
+// red_single: one cross-wave reduction buffer instead of two (one more
+// barrier per unit), for plans whose activation slice leaves no room.
+size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single);
 int decode_threads();
 // Resident decode workgroups per CU for the kernel variant and LDS size
 // (0 when the variant does not exist or the runtime cannot tell).
-int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, size_t lds);
+int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree,
+                         size_t lds);
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          hipStream_t stream);

@@ -64,7 +64,7 @@ def test_status_strings_and_version(lib):
     assert lib.pw4_status_string(0) == b"ok"
     for code in (-1, -2, -3, -4, -5):
         assert lib.pw4_status_string(code) != b"unknown status"
-    assert lib.pw4_abi_version() == 1
+    assert lib.pw4_abi_version() == 2
 
 
 def test_marlin_words_matches_oracle(lib, orc):
