@@ -141,16 +141,28 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
             }
         }
         // Exchange-tree slices (no partial round trip, no ring drain): a power
-        // of two up to 8 over 16-column units, one output element per thread.
+        // of two up to 8, M <= 32 (tree kernels exist for 16- and 32-row
+        // tiles), at most two output elements per thread.  Units as wide as
+        // that allows while every CU still gets three unit slices to balance
+        // over: a wider unit gives each K wave more steps between unit ends
+        // (measured: gate_up at M = 32 30 us with 32-column units against 37
+        // with 16; qkv and o, one slice per CU at 32 columns, are faster at 16).
         bool tree = false;
+        int tree_nb = 16;
         if (!forced) {
             int64_t s2 = std::max<int64_t>(s, decode_splits_override());
             if (s2 > 1) {
                 int64_t p2 = 2;
                 while (p2 < s2) p2 *= 2;
-                const int64_t ncg16 = ceil_div(ncols, 16);
-                if (p2 <= 8 && p2 <= steps && M * 16 <= 512 &&
-                    (size_t)(p2 - 1) * ncg16 * M * 16 * sizeof(uint64_t) <= kSlotBytes) {
+                for (int w : {64, 32, 16}) {
+                    if (M * w <= 1024 && ncols % w == 0 && (ceil_div(ncols, w) * p2 >= 3 * cus || w == 16)) {
+                        tree_nb = w;
+                        break;
+                    }
+                }
+                const int64_t ncgw = ceil_div(ncols, tree_nb);
+                if (p2 <= 8 && p2 <= steps && M <= 32 && M * tree_nb <= 1024 &&
+                    (size_t)(p2 - 1) * ncgw * M * tree_nb * sizeof(uint64_t) <= kSlotBytes) {
                     s = p2;
                     tree = true;
                 }
@@ -161,7 +173,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         const size_t lds = lds_for(s);
         // Units: 16 columns (eight K waves per strip, the finest balance), or
         // 64 when K is sliced, to keep the per-unit partial round trips few.
-        int nb = tree ? 16 : decode_nb_override();
+        int nb = tree ? tree_nb : decode_nb_override();
         if (nb == 0) nb = s > 1 ? 64 : 16;
         while (nb > 16 && ncols % nb != 0) nb /= 2;
         const int64_t ncg = ceil_div(ncols, nb);

@@ -420,36 +420,41 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     };
 
     // ---- K slices through a pairwise exchange tree ---------------------------
-    // splits = 2^levels, one output element per thread (M * nb <= 512).  At
-    // level l the slices pair up as subtrees of 2^l: each side swaps its sum
-    // for the 64-bit slot's previous content {value, flag}; the side that
-    // finds its partner's value adds it (a + b == b + a in fp32, so the sum
-    // does not depend on who came first), clears the slot and goes up a
-    // level; after the top level it stores y.  Value and flag travel in one
-    // atomic, so nothing else needs ordering.  A swap's answer is read one
-    // unit later: by then only weight loads issued after it are outstanding,
-    // and in-order vmcnt lets the wave wait for the swap alone instead of
-    // draining the ring.
+    // splits = 2^levels; output element i = tid + 512 e of the unit, e < 2
+    // (M * nb <= 1024).  At level l the slices pair up as subtrees of 2^l:
+    // each side swaps its sum for the 64-bit slot's previous content {value,
+    // flag}; the side that finds its partner's value adds it (a + b == b + a
+    // in fp32, so the sum does not depend on who came first), clears the
+    // slot and goes up a level; after the top level it stores y.  Value and
+    // flag travel in one atomic, so nothing else needs ordering.  A swap's
+    // answer is read one unit later: by then only weight loads issued after
+    // it are outstanding, and in-order vmcnt lets the wave wait for the swap
+    // alone instead of draining the ring.
     constexpr int kMaxLevels = 3;
+    constexpr int kMaxE = 2;
     const int levels = a.tree_levels;
-    uint64_t t_old[kMaxLevels + 1];
-    float t_v[kMaxLevels + 1];
-    bool t_alive[kMaxLevels + 1];
+    const int nout_all = M * nb;
+    uint64_t t_old[kMaxLevels + 1][kMaxE];
+    float t_v[kMaxLevels + 1][kMaxE];
+    bool t_alive[kMaxLevels + 1][kMaxE];
     int t_cg[kMaxLevels + 1];  // unit of the stage (wave-uniform), -1 when empty
 #pragma unroll
     for (int k = 0; k <= kMaxLevels; ++k) {
-        t_old[k] = 0;
-        t_v[k] = 0.f;
-        t_alive[k] = false;
         t_cg[k] = -1;
+#pragma unroll
+        for (int e = 0; e < kMaxE; ++e) {
+            t_old[k][e] = 0;
+            t_v[k][e] = 0.f;
+            t_alive[k][e] = false;
+        }
     }
-    auto slot = [&](int level, int cg) {
+    auto slot = [&](int level, int cg, int i) {
         const int node = (a.splits - (a.splits >> level)) + (split >> (level + 1));
-        return a.slots + (((int64_t)node * a.ncg + cg) * (M * nb) + tid);
+        return a.slots + (((int64_t)node * a.ncg + cg) * nout_all + i);
     };
-    auto swap_in = [&](int level, int cg, float v) -> uint64_t {
+    auto swap_in = [&](int level, int cg, int i, float v) -> uint64_t {
         const unsigned long long mine = (unsigned long long)__builtin_bit_cast(uint32_t, v) | (1ull << 32);
-        return __hip_atomic_exchange(slot(level, cg), mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return __hip_atomic_exchange(slot(level, cg, i), mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     auto tree_advance = [&]() {
 #pragma unroll
@@ -457,24 +462,28 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
             if (k >= levels || t_cg[k] < 0) continue;
             const int cg = t_cg[k];
             t_cg[k] = -1;
-            bool go = false;
-            float v = 0.f;
-            if (t_alive[k]) {
-                if ((t_old[k] >> 32) != 0) {  // the partner was first: combine, clear the slot
-                    v = __builtin_bit_cast(float, (uint32_t)t_old[k]) + t_v[k];
-                    __hip_atomic_store(slot(k, cg), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    go = true;
+            if (k + 1 < levels) t_cg[k + 1] = cg;  // stage k + 1 was emptied earlier in this loop
+#pragma unroll
+            for (int e = 0; e < kMaxE; ++e) {
+                const int i = tid + e * kThreads;
+                bool go = false;
+                float v = 0.f;
+                if (t_alive[k][e]) {
+                    if ((t_old[k][e] >> 32) != 0) {  // the partner was first: combine, clear the slot
+                        v = __builtin_bit_cast(float, (uint32_t)t_old[k][e]) + t_v[k][e];
+                        __hip_atomic_store(slot(k, cg, i), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        go = true;
+                    }
+                    t_alive[k][e] = false;
                 }
-                t_alive[k] = false;
-            }
-            if (k + 1 < levels) {  // stage k + 1 was emptied earlier in this loop
-                t_cg[k + 1] = cg;
-                t_alive[k + 1] = go;
-                t_v[k + 1] = v;
-                if (go) t_old[k + 1] = swap_in(k + 1, cg, v);
-            } else if (go) {
-                const int row = tid >> (4 + cwn_log2), n = cg * nb + (tid & (nb - 1));
-                if (n < N) a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
+                if (k + 1 < levels) {
+                    t_alive[k + 1][e] = go;
+                    t_v[k + 1][e] = v;
+                    if (go) t_old[k + 1][e] = swap_in(k + 1, cg, i, v);
+                } else if (go) {
+                    const int row = i >> (4 + cwn_log2), n = cg * nb + (i & (nb - 1));
+                    if (n < N) a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
+                }
             }
         }
     };
@@ -511,12 +520,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
         };
         if constexpr (TREE) {
             tree_advance();
-            const bool mine = tid < nout;
-            const float v = mine ? reduced(tid) : 0.f;
             t_cg[0] = cg;
-            t_v[0] = v;
-            t_alive[0] = mine;
-            if (mine) t_old[0] = swap_in(0, cg, v);
+#pragma unroll
+            for (int e = 0; e < kMaxE; ++e) {
+                const int i = tid + e * kThreads;
+                const bool mine = i < nout;
+                const float v = mine ? reduced(i) : 0.f;
+                t_v[0][e] = v;
+                t_alive[0][e] = mine;
+                if (mine) t_old[0][e] = swap_in(0, cg, i, v);
+            }
             return;
         }
         if (a.partial == nullptr) {

@@ -61,10 +61,20 @@ def test_stack_graph_matches_oracle(m):
             check(y, y_ref, torch.float16, f"stack m={m} k={k}")
 
 
+def _close16(a, b):
+    # Fused and separate linears may get different plans (unit width, K
+    # slices), hence a different fp32 summation order: equal up to the fp16
+    # rounding of the output (one ulp, 2^-10 relative), or, for outputs near
+    # zero after cancellation, up to the reordering error of fp32 sums whose
+    # terms are O(1) (1e-4 absolute).
+    torch.testing.assert_close(a.float(), b.float(), rtol=2 ** -10, atol=1e-4)
+
+
 @pytest.mark.parametrize("m", [1, 32])
 def test_fused_stack_equals_unfused(m):
-    """q|k|v and gate|up fused along N compute every column exactly as the
-    separate linears do (same K, same per-column reduction)."""
+    """q|k|v and gate|up fused along N compute every column as the separate
+    linears do, to the last bit where the plans agree and within one fp16 ulp
+    where they do not."""
     layers = random_layers(1, device="cuda:0", seed=5)
     fused = fuse_layers(layers)
     assert [(l.name, l.k, l.n) for l in fused[0]] == [("qkv", 4096, 6144), ("o", 4096, 4096),
@@ -79,7 +89,11 @@ def test_fused_stack_equals_unfused(m):
     b.step()
     torch.cuda.synchronize()
     ya, yb = a.outputs, b.outputs
-    torch.testing.assert_close(yb[0], torch.cat(ya[0:3], dim=1), rtol=0, atol=0)
+    _close16(yb[0], torch.cat(ya[0:3], dim=1))
+    _close16(yb[2], torch.cat(ya[4:6], dim=1))
+    # o and down are the same linear in both stacks: same plan, same bits
     torch.testing.assert_close(yb[1], ya[3], rtol=0, atol=0)
-    torch.testing.assert_close(yb[2], torch.cat(ya[4:6], dim=1), rtol=0, atol=0)
     torch.testing.assert_close(yb[3], ya[6], rtol=0, atol=0)
+    if m == 1:  # one K slice, 16-column units for every shape: identical plans
+        torch.testing.assert_close(yb[0], torch.cat(ya[0:3], dim=1), rtol=0, atol=0)
+        torch.testing.assert_close(yb[2], torch.cat(ya[4:6], dim=1), rtol=0, atol=0)
