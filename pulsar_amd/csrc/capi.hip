@@ -202,6 +202,10 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
                 best_wps = wps;
             }
         }
+        if (const char* e = std::getenv("PW4_DECODE_WPS")) {  // tuning sweeps only
+            const int64_t v = std::atoll(e);
+            if (v >= 1 && v <= 4 * (int64_t)cus) best_wps = std::min<int64_t>(v, ncg);
+        }
         dc.nb = nb;
         dc.wps = (int)best_wps;
         dc.k_per_split = (int)kps;
