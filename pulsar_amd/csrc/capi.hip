@@ -337,6 +337,9 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.nchunks = (int)ceil_div(kext, 64);
         a.chunks_per_split = p.p_cps;
         a.splits = p.p_splits;
+        a.n_begin = 0;
+        a.n_end = (int)N;
+        a.cus = cu_count();
         e = p.p256 ? launch_prefill256(stype, qzeros != nullptr, a, stream)
                    : launch_prefill(layout, xt, stype, qzeros != nullptr, a, stream);
         if (e != hipSuccess) return hip_fail(e);

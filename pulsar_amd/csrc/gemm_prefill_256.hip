@@ -29,6 +29,8 @@
 //
 // Reference counterpart: w4a16_marlin_kernel at BM = 64
 // (pulsar-core/src/kernels/w4a16_marlin.cu:197-304).
+#include <algorithm>
+
 #include "w4a16_common.h"
 #include "w4a16_kernels.h"
 
@@ -36,9 +38,8 @@ namespace pw4 {
 namespace {
 
 constexpr int kT = 256;
-constexpr int TM = 256, TN = 256, TK = 64;
+constexpr int TM = 256, TN = 256, TK = 64;  // full tile; the tail variant has TM = 128
 constexpr int kStages = 3;
-constexpr int kAStage = TM * TK * 2;  // bytes
 constexpr int kBStage = TN * TK / 2;
 constexpr int kSStage = 4 * 256;      // per wave 256 bytes of scales (64 fp32, or 64 fp16 + pad)
 constexpr int kZStage = 4 * 256;      // per wave 256 bytes of zero-point words (8 used)
@@ -81,14 +82,18 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-template <typename ST, bool ZP, bool PARTIAL>
+// RT = 32-row MFMA tiles per wave: 8 (256-row tile) or 4 (128-row tile, for
+// the N columns of the last wave; see launch_prefill256).
+template <typename ST, bool ZP, bool PARTIAL, int RT>
 __global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
+    constexpr int TMR = 32 * RT;                 // rows of this tile
+    constexpr int kAStage = TMR * TK * 2;        // bytes
     __shared__ __attribute__((aligned(16))) uint8_t sA[kStages][kAStage];
     __shared__ __attribute__((aligned(16))) uint8_t sB[kStages][kBStage];
     __shared__ __attribute__((aligned(16))) uint8_t sS[kStages][kSStage];
     __shared__ __attribute__((aligned(16))) uint8_t sZ[kStages][kZStage];
-    // copies per wave per chunk: 8 activation, 2 weight, 1 scale, 1 zero point
-    constexpr int kCopies = 8 + 2 + 1 + (ZP ? 1 : 0);
+    // copies per wave per chunk: RT activation, 2 weight, 1 scale, 1 zero point
+    constexpr int kCopies = RT + 2 + 1 + (ZP ? 1 : 0);
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -97,7 +102,8 @@ __global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, con
     const int M = a.M, N = a.N, K = a.K;
 
     // ---- tile order: XCD-aware, then grouped along M for L2 reuse ----------
-    const int num_m = (M + TM - 1) / TM, num_n = (N + TN - 1) / TN;
+    // this launch covers columns [n_begin, n_end) of the output
+    const int num_m = (M + TMR - 1) / TMR, num_n = (a.n_end - a.n_begin + TN - 1) / TN;
     const int nwg = num_m * num_n;
     int pid = blockIdx.x;
     if ((nwg & 7) == 0) pid = (pid & 7) * (nwg >> 3) + (pid >> 3);  // consecutive tiles share an XCD
@@ -106,8 +112,8 @@ __global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, con
     const int first_m = group * GM;
     const int gsz = min(num_m - first_m, GM);
     const int in_group = pid - group * GM * num_n;
-    const int m0 = (first_m + in_group % gsz) * TM;
-    const int n0 = (in_group / gsz) * TN;
+    const int m0 = (first_m + in_group % gsz) * TMR;
+    const int n0 = a.n_begin + (in_group / gsz) * TN;
 
     const int split = blockIdx.z;
     const int c_begin = split * a.chunks_per_split;
@@ -123,10 +129,10 @@ __global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, con
     // Rows past M, columns past N read clamped addresses; their results are
     // never stored.
     auto issue = [&](int kc, int st) {
-        const uint32_t abase = lds_addr(&sA[st][0]) + wave * 512 * 16;
+        const uint32_t abase = lds_addr(&sA[st][0]) + wave * RT * 1024;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int row = wave * 64 + i * 8 + (lane >> 3);
+        for (int i = 0; i < RT; ++i) {
+            const int row = wave * (8 * RT) + i * 8 + (lane >> 3);
             const int kch = (lane & 7) ^ (row & 7);
             const int gm = min(m0 + row, M - 1);
             lds_copy16(a.x + (int64_t)gm * K + kc * TK + kch * 8, abase + i * 64 * 16);
@@ -148,9 +154,9 @@ __global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, con
         }
     };
 
-    f32x16 acc[8][2];
+    f32x16 acc[RT][2];
 #pragma unroll
-    for (int rt = 0; rt < 8; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
@@ -188,10 +194,10 @@ __global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, con
             if constexpr (ZP) z = (*reinterpret_cast<const uint32_t*>(&sZ[st][wave * 256 + (cl >> 3) * 4]) >> (4 * (cl & 7))) & 0xfu;
             z2[ct] = as_h2((0x6400u | z) * 0x10001u);  // 1024 + z
         }
-        auto load_a = [&](int s, u32x4 (&av)[8]) {
+        auto load_a = [&](int s, u32x4 (&av)[RT]) {
             const int kch = 2 * s + hb;
 #pragma unroll
-            for (int rt = 0; rt < 8; ++rt) {
+            for (int rt = 0; rt < RT; ++rt) {
                 const int row = rt * 32 + c;
                 av[rt] = *reinterpret_cast<const u32x4*>(A + row * (TK * 2) + ((kch ^ (row & 7)) * 16));
             }
@@ -206,7 +212,7 @@ __global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, con
                     bv[ct][tg] = as_u32((as_h2(v) - z2[ct]) * s2[ct]);
                 }
         };
-        u32x4 av[2][8], bv[2][2];
+        u32x4 av[2][RT], bv[2][2];
         load_a(0, av[0]);
         dequant(0, bv[0]);
 #pragma unroll
@@ -217,18 +223,18 @@ __global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, con
                 dequant(s + 1, bv[cur ^ 1]);
             }
 #pragma unroll
-            for (int rt = 0; rt < 8; ++rt)
+            for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
                 for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = mfma32x32x16<false>(av[cur][rt], bv[cur][ct], acc[rt][ct]);
             // interleave: per A fragment of the next step, two MFMAs and its
             // dequant share
             if (s < 3) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+                for (int i = 0; i < RT; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);         // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 32 / RT, 0);  // VALU
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -253,7 +259,7 @@ __global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, con
     // Range-checked buffer stores: the resource covers rows [m0, M) of the
     // output (below 2 GiB), so rows past M are dropped by the hardware; lanes
     // whose column is past N start at 2 GiB, beyond the range.
-    const int rows = min(M - m0, TM);
+    const int rows = min(M - m0, TMR);
     if constexpr (!PARTIAL) {
         const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(a.y + (int64_t)m0 * N, (short)0,
                                                                             rows * N * 2, 0x00020000);
@@ -262,7 +268,7 @@ __global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, con
             const int n = ncol0 + ct * 32 + c;
             const uint32_t base = n < N ? (uint32_t)(4 * hb * N + n) * 2u : 0x80000000u;
 #pragma unroll
-            for (int rt = 0; rt < 8; ++rt) {
+            for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int r = rt * 32 + 8 * (e >> 2) + (e & 3);  // row offset without 4 * hb
@@ -281,7 +287,7 @@ __global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, con
             const int n = ncol0 + ct * 32 + c;
             const uint32_t base = n < N ? (uint32_t)(4 * hb * N + n) * 4u : 0x80000000u;
 #pragma unroll
-            for (int rt = 0; rt < 8; ++rt) {
+            for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int r = rt * 32 + 8 * (e >> 2) + (e & 3);
@@ -308,23 +314,60 @@ bool prefill256_ok(int layout, int xtype, int64_t N, int64_t K, int64_t G) {
 
 int prefill256_tile() { return TM; }
 
+// Tail balancing.  With the 256 x 256 tile, a tile count that is not a
+// multiple of the CU count leaves a partial last wave (qkv at M = 4096: 384
+// tiles on 256 CUs, 1.5 waves run as 2).  The last nt N-tile columns are then
+// done by a second launch with 128-row tiles: twice the workgroups at half the
+// work each, filling the last wave (qkv: 256 full tiles, then 256 half tiles).
+// Same arithmetic per output element, so the result does not change.
 template <typename ST, bool ZP>
-void launch_variant(const PrefillArgs& a, dim3 grid, hipStream_t stream) {
+void launch_variant(const PrefillArgs& a, hipStream_t stream) {
     const NibbleMasks mk{};
-    if (a.partial != nullptr) {
-        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, true>), grid, dim3(kT), 0, stream, a, mk);
-    } else {
-        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, false>), grid, dim3(kT), 0, stream, a, mk);
+    const int64_t num_m = ceil_div(a.M, TM), num_n = ceil_div(a.N, TN);
+    if (a.partial != nullptr) {  // K slices: full tiles, fp32 partials
+        PrefillArgs f = a;
+        f.n_begin = 0;
+        f.n_end = a.N;
+        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, true, 8>), dim3((unsigned)(num_m * num_n), 1, a.splits), dim3(kT),
+                           0, stream, f, mk);
+        return;
+    }
+    int64_t nt = 0;
+    if (a.cus > 0) {
+        // cost in waves of full tiles; a half tile counts 0.55 (its dequant
+        // is shared by half the MFMAs), and a split must save 0.1 wave
+        double best = (double)ceil_div(num_m * num_n, a.cus);
+        for (int64_t t = 1; t <= num_n; ++t) {
+            const double cost = (double)ceil_div(num_m * (num_n - t), a.cus) +
+                                0.55 * (double)ceil_div(ceil_div(a.M, TM / 2) * t, a.cus);
+            if (cost < best - 0.1) {
+                best = cost;
+                nt = t;
+            }
+        }
+    }
+    const int64_t nfull = num_n - nt;
+    if (nfull > 0) {
+        PrefillArgs f = a;
+        f.n_begin = 0;
+        f.n_end = (int)std::min<int64_t>(a.N, nfull * TN);
+        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, false, 8>), dim3((unsigned)(num_m * nfull)), dim3(kT), 0, stream,
+                           f, mk);
+    }
+    if (nt > 0) {
+        PrefillArgs h = a;
+        h.n_begin = (int)(nfull * TN);
+        h.n_end = a.N;
+        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, false, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * nt)), dim3(kT),
+                           0, stream, h, mk);
     }
 }
 
 hipError_t launch_prefill256(int stype, bool zp, const PrefillArgs& a, hipStream_t stream) {
-    const int nwg = (int)(ceil_div(a.M, TM) * ceil_div(a.N, TN));
-    const dim3 grid(nwg, 1, a.splits);
     if (stype == S_F32) {
-        zp ? launch_variant<float, true>(a, grid, stream) : launch_variant<float, false>(a, grid, stream);
+        zp ? launch_variant<float, true>(a, stream) : launch_variant<float, false>(a, stream);
     } else {
-        zp ? launch_variant<_Float16, true>(a, grid, stream) : launch_variant<_Float16, false>(a, grid, stream);
+        zp ? launch_variant<_Float16, true>(a, stream) : launch_variant<_Float16, false>(a, stream);
     }
     return hipGetLastError();
 }

@@ -93,6 +93,8 @@ struct PrefillArgs {
     int nchunks;
     int chunks_per_split;    // in 64-K chunks
     int splits;
+    int n_begin, n_end;      // output columns a launch covers (set by the 256-tile launcher)
+    int cus;                 // compute units of the device (tail balancing)
 };
 
 hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream);

@@ -77,3 +77,13 @@ def test_prefill_tiles_agree():
             del os.environ["PW4_PREFILL_TILE"]
     diff = (ys[128] - ys[256]).abs().max().item()
     assert diff <= 2e-3 * ys[128].abs().max().item(), diff
+
+
+def test_prefill_tail_split():
+    """288 tiles of 256 x 256 on 256 CUs: the last N-tile columns run as a
+    second launch of 128-row tiles; every column must match the oracle."""
+    m, n, k, g = 1024, 18432, 512, 128
+    c = reference_case(m, n, k, g, torch.float16, seed=15)
+    wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float16), g)
+    y = ops.gemm_w4a16_marlin(c.x, wm, sm, g)
+    check(y, c.y_ref, torch.float16, "tail split m=1024 n=18432")
