@@ -34,6 +34,8 @@ Also reported:
                   down per layer) replayed as one HIP graph
                   per step at M = 1 and M = 32: linear-layer time per decode
                   step and its HBM GB/s;
+  act_order_70b = the Llama-3-70B layers with asymmetric int4 and act-order
+                  (BASELINE configs[3]) at M = 1, 16 (GB/s) and 2048 (TFLOP/s);
   cpu_baseline  = the reference CPU path (dequantize to fp32, fp32 GEMM --
                   the reference test oracle restated in oracle/) on this
                   host's cores over a bounded sample of the sweep.
@@ -56,6 +58,8 @@ HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2516.6
 
 LLAMA8B = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 28672), ("down", 14336, 4096)]
+LLAMA70B = [("qkv", 8192, 10240), ("gate_up", 8192, 57344), ("down", 28672, 8192)]
+ACT_ORDER_M = [1, 16, 2048]
 DECODE_M = [1, 4, 8, 16]
 PREFILL_M = [256, 1024, 4096]
 STACK_LAYERS = 32
@@ -249,6 +253,91 @@ def stack_bench(torch, dev, steps: int, warmup: int) -> dict:
     return out
 
 
+def act_order_bytes(m: int, k: int, n: int, g: int = G) -> int:
+    """Algorithmic HBM bytes of one asymmetric act-order call: int4 weights,
+    fp16 scales, int4 zero points, the int32 K permutation, x and y."""
+    return n * k // 2 + n * (k // g) * 2 + n * (k // g) // 2 + k * 4 + m * k * 2 + m * n * 2
+
+
+def act_order_bench(torch, dev, steps: int, warmup: int) -> dict:
+    """Config 4: asymmetric int4 with act-order on the Llama-3-70B layers.
+
+    Weights are GPTQ checkpoints (qweight [K/8,N], qzeros [K/G,N/8], fp16 scales
+    [K/G,N], g_idx[p[i]] = i/G for a random permutation p) repacked with
+    repack_w4a16_gptq.  Each layer has enough copies that R copies hold
+    >= 512 MB, rotated per launch.  M = 1, 16: HBM GB/s of the graph period of
+    back-to-back launches; M = 2048: TFLOP/s of event-bracketed launches."""
+    import pulsar_amd
+
+    out = {"workload": "llama3-70b qkv 8192x10240, gate_up 8192x57344, down 28672x8192; asymmetric int4 "
+                       "G=128, fp16 scales, int4 zero points, act-order g_idx", "layers": {}}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    for name, k, n in LLAMA70B:
+        copies = max(2, -(-(512 << 20) // act_order_bytes(1, k, n)))
+        ws = []
+        for _ in range(copies):
+            qweight = torch.randint(-(2 ** 31), 2 ** 31, (k // 8, n), dtype=torch.int32, device=dev, generator=gen)
+            p = torch.randperm(k, device=dev, generator=gen)
+            g_idx = torch.empty(k, dtype=torch.int32, device=dev)
+            g_idx[p] = torch.arange(k, device=dev, dtype=torch.int32) // G
+            wm, perm = pulsar_amd.ops.repack_w4a16_gptq(qweight, g_idx, G)
+            qz = torch.randint(-(2 ** 31), 2 ** 31, (k // G, n // 8), dtype=torch.int32, device=dev, generator=gen)
+            sc = (torch.randn(k // G, n, device=dev, generator=gen) * 0.02).abs_().add_(1e-3).half()
+            ws.append((wm, sc, qz, perm))
+            del qweight, p, g_idx
+        stream = torch.cuda.Stream(device=dev)
+        res = {"copies": copies}
+        for m in ACT_ORDER_M:
+            x = torch.randn(m, k, device=dev, generator=gen).half()
+
+            def call(i):
+                w = ws[i % copies]
+                return pulsar_amd.ops.gemm_w4a16_gptq(x, w[0], w[1], w[2], w[3], G)
+
+            if m <= 16:
+                with torch.cuda.stream(stream):
+                    for i in range(copies):
+                        call(i)
+                stream.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    outs = [call(i) for i in range(copies)]
+                for _ in range(warmup):
+                    graph.replay()
+                torch.cuda.synchronize()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                with torch.cuda.stream(stream):
+                    a.record(stream)
+                    for _ in range(steps):
+                        graph.replay()
+                    b.record(stream)
+                torch.cuda.synchronize()
+                us = a.elapsed_time(b) * 1e3 / (steps * copies)
+                gbs = act_order_bytes(m, k, n) / (us * 1e-6) / 1e9
+                res[f"m{m}"] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
+                del graph, outs
+            else:
+                for i in range(2):
+                    call(i)
+                ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                      for _ in range(max(steps, 4))]
+                for i, (a, b) in enumerate(ev):
+                    a.record()
+                    call(i)
+                    b.record()
+                torch.cuda.synchronize()
+                us = sum(a.elapsed_time(b) for a, b in ev) / len(ev) * 1e3
+                tf = 2.0 * m * n * k / (us * 1e-6) / 1e12
+                res[f"m{m}"] = {"us": round(us, 1), "TFLOP/s": round(tf, 1),
+                                "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3)}
+            del x
+        out["layers"][name] = res
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def time_each_launch(torch, shapes, weights, xs, fn, stream, reps: int) -> list[float]:
     """Mean duration (ms) of single launches, each bracketed by HIP events on
     the launch stream: the kernel's own time without the back-to-back launch
@@ -278,6 +367,7 @@ def main() -> int:
     ap.add_argument("--no-reference-api", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=10)
     ap.add_argument("--no-stack", action="store_true")
+    ap.add_argument("--no-act-order", action="store_true", help="skip the 70B act-order layers (configs[3])")
     ap.add_argument("--pmc-workload", choices=["decode", "prefill"],
                     help="no timing: decode = the decode sweep's launches once each, then a 512 MiB copy (the "
                          "HBM counter calibration), for rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE; prefill = "
@@ -393,6 +483,8 @@ def main() -> int:
     if not args.no_stack:
         stack = stack_bench(torch, dev, args.steps, args.warmup)
 
+    act_order = None if args.no_act_order else act_order_bench(torch, dev, args.steps, args.warmup)
+
     cpu = None if args.no_cpu else cpu_baseline()
     if cpu is not None:
         cpu["model"] = cpu_model()
@@ -433,6 +525,7 @@ def main() -> int:
         "reference_api": ref_api,
         "prefill": prefill,
         "stack": stack,
+        "act_order_70b": act_order,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

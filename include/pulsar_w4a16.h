@@ -4,7 +4,10 @@
  *
  * Plain pointers and sizes only: every tensor argument is a device pointer
  * (hipMalloc'd or torch-owned), every size is an element count, every call is
- * asynchronous on `stream` and returns 0 or a negative PW4_ERR_* status.  No
+ * asynchronous on `stream` and returns 0 or a negative PW4_ERR_* status.  The
+ * GEMMs read x and the weight words as 16-byte vectors: those two pointers
+ * must be 16-byte aligned (any allocation is, and so is any row slice of x
+ * since K % 8 == 0), else the call returns PW4_ERR_ARG.  No
  * entry point allocates device memory: scratch space is passed in through
  * (workspace, workspace_bytes) and sized with the matching *_workspace_size
  * query, so the GEMMs are safe under HIP graph capture.
@@ -36,7 +39,7 @@ typedef struct ihipStream_t* pw4_stream_t; /* == hipStream_t */
 
 /* status codes */
 #define PW4_OK 0
-#define PW4_ERR_ARG (-1)       /* null pointer, unknown dtype, negative size */
+#define PW4_ERR_ARG (-1)       /* null or misaligned pointer, unknown dtype, negative size */
 #define PW4_ERR_SHAPE (-2)     /* inconsistent sizes / group size (reference TORCH_CHECKs) */
 #define PW4_ERR_WORKSPACE (-3) /* workspace missing or smaller than the *_workspace_size query */
 #define PW4_ERR_HIP (-4)       /* a HIP runtime call or kernel launch failed */

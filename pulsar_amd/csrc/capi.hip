@@ -154,8 +154,11 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
             if (s2 > 1) {
                 int64_t p2 = 2;
                 while (p2 < s2) p2 *= 2;
+                const int nb_forced = decode_nb_override();
                 for (int w : {64, 32, 16}) {
-                    if (M * w <= 1024 && ncols % w == 0 && (ceil_div(ncols, w) * p2 >= 3 * cus || w == 16)) {
+                    const bool fits = M * w <= 1024 && ncols % w == 0;
+                    if (nb_forced ? (w == nb_forced && fits) || w == 16
+                                  : fits && (ceil_div(ncols, w) * p2 >= 3 * cus || w == 16)) {
                         tree_nb = w;
                         break;
                     }
@@ -253,8 +256,10 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         p.splits = (int)s;
         p.use_partial = forced || s > 1;
         if (p.use_partial) p.partial_bytes = (size_t)p.splits * M * N * 4;
-        if (has_perm) p.xperm_bytes = (size_t)M * K * 2;
     }
+    // act-order: x is gathered once per call into the workspace, for either
+    // kernel (each decode workgroup would otherwise gather the same slice)
+    if (has_perm) p.xperm_bytes = (size_t)M * K * 2;
     return p;
 }
 
@@ -270,6 +275,8 @@ int check_common(int64_t M, int64_t N, int64_t K, int64_t G, int x_dtype) {
 int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const void* scales, int stype,
              const uint32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N, int64_t K, int64_t G,
              int64_t num_splits, void* workspace, size_t ws_bytes, hipStream_t stream) {
+    // x and the weight words are read as 16-byte vectors
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) return PW4_ERR_ARG;
     const Plan p = make_plan(layout, x_dtype, stype, qzeros != nullptr, M, N, K, G, perm != nullptr, num_splits);
     if (p.workspace() > 0 && (workspace == nullptr || ws_bytes < p.workspace())) return PW4_ERR_WORKSPACE;
     char* ws = reinterpret_cast<char*>(workspace);
@@ -281,13 +288,18 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
     const int xt = x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16;
     const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
     hipError_t e;
+    const uint16_t* xin = reinterpret_cast<const uint16_t*>(x);
+    if (perm) {
+        e = launch_gather_x(xin, perm, xperm, (int)M, (int)K, stream);
+        if (e != hipSuccess) return hip_fail(e);
+        xin = xperm;
+    }
     if (p.decode) {
         DecodeArgs a{};
-        a.x = reinterpret_cast<const uint16_t*>(x);
+        a.x = xin;
         a.w = w;
         a.scales = scales;
         a.qzeros = qzeros;
-        a.perm = perm;
         a.y = reinterpret_cast<uint16_t*>(y);
         a.partial = p.use_partial ? partial : nullptr;
         a.counters = counters;
@@ -315,12 +327,6 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         e = launch_decode(layout, xt, stype, qzeros != nullptr, p.dc, a, stream);
         if (e != hipSuccess) return hip_fail(e);
     } else {
-        const uint16_t* xin = reinterpret_cast<const uint16_t*>(x);
-        if (perm) {
-            e = launch_gather_x(xin, perm, xperm, (int)M, (int)K, stream);
-            if (e != hipSuccess) return hip_fail(e);
-            xin = xperm;
-        }
         PrefillArgs a{};
         a.x = xin;
         a.w = w;

@@ -212,8 +212,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     const int spr = a.k_per_split / 8 + 1;
     const int nslots = (int)x_slots(M, a.k_per_split);
     const int kvalid = max(min(klen, K - kb), 0);  // halves of real activations in the slice
-    const bool gather = a.perm != nullptr;
-    if (!gather) {
+    {
         const uint32_t smem_base = (uint32_t)(uintptr_t)smem;
         for (int b = wave; b * 64 < nslots; b += kWaves) {
             const int f = b * 64 + lane;
@@ -283,30 +282,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- finish the slice: act-order gather, zero fill, (bf16) corrections --
-    if (gather) {
-        // act-order: element gathers through registers, one slot per item
-        for (int f = tid; f < nslots; f += kThreads) {
-            const int row = f / spr, s8 = f - row * spr;
-            u32x4 v = u32x4{0u, 0u, 0u, 0u};
-            if (row < M && s8 * 8 < kvalid) {
-                uint16_t hv[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    hv[e] = a.x[(int64_t)row * K + min(max(a.perm[kb + s8 * 8 + e], 0), K - 1)];
-                }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = (uint32_t)hv[2 * e] | ((uint32_t)hv[2 * e + 1] << 16);
-            }
-            *reinterpret_cast<u32x4*>(smem + f * 8) = v;
-        }
+    // ---- finish the slice: zero fill, (bf16) corrections ---------------------
+    if constexpr (LAYOUT == LAYOUT_MARLIN) {
+        wait_vmcnt<U * kLoadsPerStep>();  // this wave's slice copies are done; its ring is still in flight
     } else {
-        if constexpr (LAYOUT == LAYOUT_MARLIN) {
-            wait_vmcnt<U * kLoadsPerStep>();  // this wave's slice copies are done; its ring is still in flight
-        } else {
-            wait_vmcnt<0>();
-        }
-        // zero the slots the steps read past the real activations
+        wait_vmcnt<0>();
+    }
+    // zero the slots the steps read past the real activations
+    {
         const int zfrom = kvalid / 8, zto = nsteps * 16;
         for (int i = tid; i < M * (zto - zfrom); i += kThreads) {
             const int row = i / (zto - zfrom), s8 = zfrom + (i - row * (zto - zfrom));

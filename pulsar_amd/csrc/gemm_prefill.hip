@@ -268,13 +268,28 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) 
         }
 }
 
+// x_out[m, j..j+8) = x[m, perm[j..j+8)]: one 16-byte store per thread (K % 8
+// == 0 on every path; the output is a 256-byte aligned workspace).  The 8
+// element reads of a thread are independent, so they are in flight together.
 __global__ __launch_bounds__(256) void gather_x_kernel(const uint16_t* __restrict__ x, const int32_t* __restrict__ perm,
                                                        uint16_t* __restrict__ out, int M, int K) {
+    const int k8 = K >> 3;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)M * K) return;
-    const int64_t m = i / K;
-    const int j = (int)(i - m * K);
-    out[i] = x[m * K + min(max(perm[j], 0), K - 1)];  // clamped: a bad perm cannot fault
+    if (i >= (int64_t)M * k8) return;
+    const int64_t m = i / k8;
+    const int j = (int)(i - m * k8) * 8;
+    int idx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) idx[e] = perm[j + e];
+    const uint16_t* row = x + m * K;
+    uint32_t v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = row[min(max(idx[2 * e], 0), K - 1)];  // clamped: a bad perm cannot fault
+        const uint32_t hi = row[min(max(idx[2 * e + 1], 0), K - 1)];
+        v[e] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4*>(out + m * K + j) = make_uint4(v[0], v[1], v[2], v[3]);
 }
 
 template <bool BF16, int LAYOUT, typename ST, bool ZP>
@@ -309,7 +324,8 @@ hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const Prefi
 }
 
 hipError_t launch_gather_x(const uint16_t* x, const int32_t* perm, uint16_t* out, int M, int K, hipStream_t stream) {
-    const int64_t n = (int64_t)M * K;
+    if (K % 8 != 0) return hipErrorInvalidValue;
+    const int64_t n = (int64_t)M * (K / 8);
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(gather_x_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, x, perm, out, M, K);
     return hipGetLastError();

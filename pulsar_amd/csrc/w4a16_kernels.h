@@ -25,11 +25,10 @@ struct NibbleMasks {
 };
 
 struct DecodeArgs {
-    const uint16_t* x;       // [M, K] fp16 / bf16 bits
+    const uint16_t* x;       // [M, K] fp16 / bf16 bits (already act-order permuted when needed)
     const uint32_t* w;       // MARLIN words, or CT [N, K/8]
     const void* scales;      // MARLIN: [Kg, N]; CT: [N, Kg] fp32
     const uint32_t* qzeros;  // [Kg, N/8] (MARLIN, asymmetric) or null
-    const int32_t* perm;     // [K] act-order gather of x, or null
     uint16_t* y;             // [M, N] output
     float* partial;          // [ncg, splits, M, nb] fp32, or null for the direct store
     int32_t* counters;       // [ncg] arrival counters (zero on entry, left zero)

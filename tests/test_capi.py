@@ -84,6 +84,11 @@ def test_argument_checks_fire_before_launch(lib):
     assert lib.pw4_gemm_w4a16(dummy, 7, dummy, dummy, dummy, 4, 64, 128, 64, 0, None, 0, None) == -1
     assert lib.pw4_gemm_w4a16(None, 0, dummy, dummy, dummy, 4, 64, 128, 64, 0, None, 0, None) == -1
     assert lib.pw4_gemm_w4a16(dummy, 0, dummy, dummy, dummy, 4, 64, 128, 64, -1, None, 0, None) == -1
+    # x and the weight words must be 16-byte aligned (read as 16-byte vectors)
+    odd = ctypes.c_void_p(18)
+    assert lib.pw4_gemm_w4a16(odd, 0, dummy, dummy, dummy, 4, 64, 128, 64, 0, None, 0, None) == -1
+    assert lib.pw4_gemm_w4a16_marlin(dummy, 0, odd, dummy, 2, None, None, dummy, 4, 64, 128, 64, 0, None, 0,
+                                     None) == -1
     # M == 0 and N == 0 are no-ops (w4a16_gemm.cu:355-357)
     assert lib.pw4_gemm_w4a16(None, 0, None, None, None, 0, 64, 128, 64, 0, None, 0, None) == 0
     assert lib.pw4_gemm_w4a16(None, 0, None, None, None, 4, 0, 128, 64, 0, None, 0, None) == 0
@@ -109,6 +114,9 @@ def test_workspace_queries(lib):
     ws_perm = lib.pw4_gemm_w4a16_marlin_workspace_size(512, 256, 512, 64, 1, 0)
     ws_noperm = lib.pw4_gemm_w4a16_marlin_workspace_size(512, 256, 512, 64, 0, 0)
     assert ws_perm >= ws_noperm + 512 * 512 * 2
+    # act-order decode gathers x once per call into the workspace as well
+    ws_perm1 = lib.pw4_gemm_w4a16_marlin_workspace_size(1, 256, 512, 64, 1, 0)
+    assert ws_perm1 >= (16 << 20) + 512 * 2
 
 
 def test_missing_workspace_is_rejected(lib):
