@@ -66,6 +66,21 @@ int prefill_tile_override() {
     return (v == 128 || v == 256) ? v : 0;
 }
 
+// Rows of the 256-wide prefill tiles (256 or 128) and the K-slice count of
+// an unforced prefill plan (1..64), for tuning sweeps; 0 = heuristic.
+int prefill_rows_override() {
+    const char* e = std::getenv("PW4_PREFILL_ROWS");
+    if (!e) return 0;
+    const int v = std::atoi(e);
+    return (v == 128 || v == 256) ? v : 0;
+}
+int prefill_splits_override() {
+    const char* e = std::getenv("PW4_PREFILL_SPLITS");
+    if (!e) return 0;
+    const int v = std::atoi(e);
+    return (v >= 1 && v <= 64) ? v : 0;
+}
+
 // Decode K-split override for tuning sweeps (2, 4 or 8: exchange-tree
 // slices even where the activations fit in LDS); 0 = heuristic.
 int decode_splits_override() {
@@ -75,6 +90,55 @@ int decode_splits_override() {
     return (v == 2 || v == 4 || v == 8) ? v : 0;
 }
 
+// Plan of the 256-wide prefill kernel: tile rows (256 or 128) and K slices,
+// from a cost model in microseconds fitted to a sweep of every (rows, slices)
+// pair over the Llama-3-8B layer shapes at M = 256..4096 on one MI355X:
+//   * a 64-K chunk of a 256-row tile takes 2.0 us on a CU; 256-row tiles run
+//     one workgroup per CU (126 KB of LDS), in waves of the CU count, and an
+//     unsplit launch balances its last wave with 128-row tiles;
+//   * a 128-row tile's chunk takes 0.6 of that; two such workgroups share a CU
+//     (78 KB of LDS each), which then takes 0.8 of their summed time;
+//   * K slices add their fp32 partials' round trip, s * M * N * 8 bytes at
+//     6 TB/s, plus 2 us for the combine launch.
+// Picks are within 1% of the sweep's best in total (3682 against 3660 us over
+// 20 shapes; the former fixed rule took 3888).
+struct Prefill256Plan {
+    int rows;
+    int64_t splits;
+};
+
+Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus) {
+    constexpr double kChunkUs = 2.0, kHalfChunk = 0.6, kShare = 0.8, kPartialBps = 6.0e12, kCombineUs = 2.0;
+    Prefill256Plan best{256, 1};
+    double best_us = 0.0;
+    bool have = false;
+    const int64_t num_n = ceil_div(N, 256);
+    for (int rows : {256, 128}) {
+        for (int64_t s : {1, 2, 3, 4, 6, 8}) {
+            if (s > nchunks) break;
+            const int64_t cps = ceil_div(nchunks, s);
+            const int64_t sl = ceil_div(nchunks, cps);
+            if (s > 1 && sl != s) continue;  // the same plan as a smaller s
+            double us;
+            if (rows == 256) {
+                double waves = (double)ceil_div(ceil_div(M, 256) * num_n * s, cus);
+                if (s == 1) prefill256_tail_cols(M, N, cus, &waves);
+                us = waves * (double)cps * kChunkUs;
+            } else {
+                const int64_t wgs = ceil_div(M, 128) * num_n * s;
+                us = (double)cps * kHalfChunk * kChunkUs * (wgs <= cus ? 1.0 : (double)ceil_div(wgs, cus) * kShare);
+            }
+            if (s > 1) us += (double)s * (double)M * (double)N * 8.0 / kPartialBps * 1e6 + kCombineUs;
+            if (!have || us < best_us) {
+                best = {rows, s};
+                best_us = us;
+                have = true;
+            }
+        }
+    }
+    return best;
+}
+
 struct Plan {
     bool decode = false;
     bool tree = false;       // decode K slices reduced through the exchange tree
@@ -82,6 +146,7 @@ struct Plan {
     DecodeConfig dc{};
     int p_splits = 1;        // prefill K splits
     int p_cps = 0;           // prefill chunks per split
+    int p_tile_rows = 256;   // 256-wide kernel: rows per tile
     bool use_partial = false;
     int splits = 1;
     size_t partial_bytes = 0;
@@ -144,9 +209,10 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         // of two up to 8, M <= 32 (tree kernels exist for 16- and 32-row
         // tiles), at most two output elements per thread.  Units as wide as
         // that allows while every CU still gets three unit slices to balance
-        // over: a wider unit gives each K wave more steps between unit ends
-        // (measured: gate_up at M = 32 30 us with 32-column units against 37
-        // with 16; qkv and o, one slice per CU at 32 columns, are faster at 16).
+        // over at 64 columns, two at 32: a wider unit gives each K wave more
+        // steps between unit ends (measured: gate_up at M = 32 30 us with
+        // 32-column units against 37 with 16, down at M = 16 13.8 against 15.1;
+        // qkv and o, one slice per CU at 32 columns, are faster at 16).
         bool tree = false;
         int tree_nb = 16;
         if (!forced) {
@@ -158,7 +224,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
                 for (int w : {64, 32, 16}) {
                     const bool fits = M * w <= 1024 && ncols % w == 0;
                     if (nb_forced ? (w == nb_forced && fits) || w == 16
-                                  : fits && (ceil_div(ncols, w) * p2 >= 3 * cus || w == 16)) {
+                                  : fits && (ceil_div(ncols, w) * p2 >= (w == 64 ? 3 : 2) * cus || w == 16)) {
                         tree_nb = w;
                         break;
                     }
@@ -243,6 +309,12 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         int64_t s;
         if (forced) {
             s = std::min<int64_t>(num_splits, std::max<int64_t>(nchunks, 1));  // more would be empty slices
+        } else if (p.p256 && prefill_splits_override()) {
+            s = std::min<int64_t>(prefill_splits_override(), std::max<int64_t>(nchunks, 1));
+        } else if (p.p256) {
+            const Prefill256Plan pp = plan_prefill256(M, N, nchunks, cus);
+            s = pp.splits;
+            p.p_tile_rows = pp.rows;
         } else if (base >= cus || nchunks < 8) {
             s = 1;
         } else {
@@ -256,6 +328,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         p.splits = (int)s;
         p.use_partial = forced || s > 1;
         if (p.use_partial) p.partial_bytes = (size_t)p.splits * M * N * 4;
+        if (p.p256 && prefill_rows_override()) p.p_tile_rows = prefill_rows_override();
     }
     // act-order: x is gathered once per call into the workspace, for either
     // kernel (each decode workgroup would otherwise gather the same slice)
@@ -346,6 +419,7 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.n_begin = 0;
         a.n_end = (int)N;
         a.cus = cu_count();
+        a.tile_rows = p.p_tile_rows;
         e = p.p256 ? launch_prefill256(stype, qzeros != nullptr, a, stream)
                    : launch_prefill(layout, xt, stype, qzeros != nullptr, a, stream);
         if (e != hipSuccess) return hip_fail(e);

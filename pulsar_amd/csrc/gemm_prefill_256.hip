@@ -84,8 +84,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // RT = 32-row MFMA tiles per wave: 8 (256-row tile) or 4 (128-row tile, for
 // the N columns of the last wave; see launch_prefill256).
+// 128-row tiles (RT = 4) use 78 KB of LDS, so two workgroups fit on a CU if
+// each wave keeps to 256 registers (two waves per SIMD).
 template <typename ST, bool ZP, bool PARTIAL, int RT>
-__global__ __launch_bounds__(kT) void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(RT == 4 ? 2 : 1, RT == 4 ? 2 : 1)))
+void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
     constexpr int TMR = 32 * RT;                 // rows of this tile
     constexpr int kAStage = TMR * TK * 2;        // bytes
     __shared__ __attribute__((aligned(16))) uint8_t sA[kStages][kAStage];
@@ -314,6 +317,28 @@ bool prefill256_ok(int layout, int xtype, int64_t N, int64_t K, int64_t G) {
 
 int prefill256_tile() { return TM; }
 
+// Tail balancing of an unsplit launch of 256-row tiles: the number of
+// trailing N-tile columns to run as 128-row tiles, and the cost in waves of
+// full tiles (a half tile counts 0.55: its dequant is shared by half the
+// MFMAs; a split must save 0.1 wave).
+int64_t prefill256_tail_cols(int64_t M, int64_t N, int cus, double* waves) {
+    const int64_t num_m = ceil_div(M, TM), num_n = ceil_div(N, TN);
+    double best = cus > 0 ? (double)ceil_div(num_m * num_n, cus) : 1.0;
+    int64_t nt = 0;
+    if (cus > 0) {
+        for (int64_t t = 1; t <= num_n; ++t) {
+            const double cost = (double)ceil_div(num_m * (num_n - t), cus) +
+                                0.55 * (double)ceil_div(ceil_div(M, TM / 2) * t, cus);
+            if (cost < best - 0.1) {
+                best = cost;
+                nt = t;
+            }
+        }
+    }
+    if (waves) *waves = best;
+    return nt;
+}
+
 // Tail balancing.  With the 256 x 256 tile, a tile count that is not a
 // multiple of the CU count leaves a partial last wave (qkv at M = 4096: 384
 // tiles on 256 CUs, 1.5 waves run as 2).  The last nt N-tile columns are then
@@ -324,28 +349,28 @@ template <typename ST, bool ZP>
 void launch_variant(const PrefillArgs& a, hipStream_t stream) {
     const NibbleMasks mk{};
     const int64_t num_m = ceil_div(a.M, TM), num_n = ceil_div(a.N, TN);
-    if (a.partial != nullptr) {  // K slices: full tiles, fp32 partials
+    if (a.partial != nullptr) {  // K slices: fp32 partials of 256- or 128-row tiles
         PrefillArgs f = a;
         f.n_begin = 0;
         f.n_end = a.N;
-        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, true, 8>), dim3((unsigned)(num_m * num_n), 1, a.splits), dim3(kT),
-                           0, stream, f, mk);
+        if (a.tile_rows == TM / 2) {
+            hipLaunchKernelGGL((prefill256_kernel<ST, ZP, true, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * num_n), 1,
+                                                                          a.splits), dim3(kT), 0, stream, f, mk);
+        } else {
+            hipLaunchKernelGGL((prefill256_kernel<ST, ZP, true, 8>), dim3((unsigned)(num_m * num_n), 1, a.splits),
+                               dim3(kT), 0, stream, f, mk);
+        }
         return;
     }
-    int64_t nt = 0;
-    if (a.cus > 0) {
-        // cost in waves of full tiles; a half tile counts 0.55 (its dequant
-        // is shared by half the MFMAs), and a split must save 0.1 wave
-        double best = (double)ceil_div(num_m * num_n, a.cus);
-        for (int64_t t = 1; t <= num_n; ++t) {
-            const double cost = (double)ceil_div(num_m * (num_n - t), a.cus) +
-                                0.55 * (double)ceil_div(ceil_div(a.M, TM / 2) * t, a.cus);
-            if (cost < best - 0.1) {
-                best = cost;
-                nt = t;
-            }
-        }
+    if (a.tile_rows == TM / 2) {  // every tile 128 rows: twice the workgroups, two per CU
+        PrefillArgs h = a;
+        h.n_begin = 0;
+        h.n_end = a.N;
+        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, false, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * num_n)),
+                           dim3(kT), 0, stream, h, mk);
+        return;
     }
+    const int64_t nt = prefill256_tail_cols(a.M, a.N, a.cus, nullptr);
     const int64_t nfull = num_n - nt;
     if (nfull > 0) {
         PrefillArgs f = a;

@@ -94,6 +94,7 @@ struct PrefillArgs {
     int splits;
     int n_begin, n_end;      // output columns a launch covers (set by the 256-tile launcher)
     int cus;                 // compute units of the device (tail balancing)
+    int tile_rows;           // 256-wide kernel: 256-row tiles (tail balanced when unsplit) or 128-row tiles
 };
 
 hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream);
@@ -104,6 +105,9 @@ int prefill_tile_n();
 // K and the group size multiples of 64).  Same arguments as launch_prefill.
 bool prefill256_ok(int layout, int xtype, int64_t N, int64_t K, int64_t G);
 int prefill256_tile();
+// Unsplit 256-row launches: N-tile columns run as 128-row tail tiles, and the
+// launch's cost in waves of full tiles (into *waves when not null).
+int64_t prefill256_tail_cols(int64_t M, int64_t N, int cus, double* waves);
 hipError_t launch_prefill256(int stype, bool zp, const PrefillArgs& a, hipStream_t stream);
 
 // x_out[m, j] = x[m, perm[j]]

@@ -62,6 +62,18 @@ def test_prefill_gptq(tile, sym, act, sdtype):
     check(y, c.y_ref, torch.float16, f"tile={tile} gptq sym={sym} act={act} scales={sdtype}")
 
 
+@pytest.fixture
+def plan_env():
+    keys = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS")
+    old = {k: os.environ.get(k) for k in keys}
+    yield os.environ
+    for k, v in old.items():
+        if v is None:
+            os.environ.pop(k, None)
+        else:
+            os.environ[k] = v
+
+
 def test_prefill_tiles_agree():
     """Both prefill kernels accumulate in fp32 over the same dequantized fp16
     weights; their outputs agree to fp16 output rounding."""
@@ -79,11 +91,31 @@ def test_prefill_tiles_agree():
     assert diff <= 2e-3 * ys[128].abs().max().item(), diff
 
 
-def test_prefill_tail_split():
+def test_prefill_tail_split(plan_env):
     """288 tiles of 256 x 256 on 256 CUs: the last N-tile columns run as a
     second launch of 128-row tiles; every column must match the oracle."""
+    plan_env["PW4_PREFILL_ROWS"] = "256"
+    plan_env["PW4_PREFILL_SPLITS"] = "1"
     m, n, k, g = 1024, 18432, 512, 128
     c = reference_case(m, n, k, g, torch.float16, seed=15)
     wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float16), g)
     y = ops.gemm_w4a16_marlin(c.x, wm, sm, g)
     check(y, c.y_ref, torch.float16, "tail split m=1024 n=18432")
+
+
+@pytest.mark.parametrize("rows", [256, 128])
+@pytest.mark.parametrize("splits", [1, 3, 8])
+@pytest.mark.parametrize("m,n", [(300, 520), (129, 264)])
+def test_prefill_plans_agree_with_oracle(plan_env, rows, splits, m, n):
+    """Every plan the 256-wide kernel can be given -- 256- or 128-row tiles,
+    unsplit (with 128-row tail tiles) or with K slices -- computes the same
+    GEMM: ragged M and N against the oracle, fp16 and fp32 scales."""
+    k, g = 1024, 128
+    plan_env["PW4_PREFILL_ROWS"] = str(rows)
+    plan_env["PW4_PREFILL_SPLITS"] = str(splits)
+    c = reference_case(m, n, k, g, torch.float16, seed=16)
+    wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float16), g)
+    y32 = ops.gemm_w4a16_marlin(c.x, wm, sm, g)
+    check(y32, c.y_ref, torch.float16, f"rows={rows} splits={splits} m={m} n={n} fp32 scales")
+    y16 = ops.gemm_w4a16_gptq(c.x, wm, sm.half(), None, None, g)
+    check(y16, c.y_ref, torch.float16, f"rows={rows} splits={splits} m={m} n={n} fp16 scales")
