@@ -295,12 +295,13 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
     }
     if (!p.decode) {
         const int64_t nchunks = ceil_div(kext, 64);
-        // The 256 x 256 kernel (MARLIN, fp16) needs whole 64-K chunks inside one
-        // quant group; measured faster than the 128 x 128 kernel from M = 256 on
-        // every Llama-3-8B layer shape, and used once M passes half its tile.
+        // The 256-wide kernel (MARLIN, fp16) needs whole 64-K chunks inside one
+        // quant group; with its 128-row tiles and K slices it is measured 20-45%
+        // faster than the 128 x 128 kernel at M = 72..160 on every Llama-3-8B
+        // layer shape, so it takes every M past the decode kernel's.
         const bool ok256 = prefill256_ok(layout, x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16, N, K, G);
         const int tile_pref = prefill_tile_override();
-        p.p256 = ok256 && (tile_pref == 256 || (tile_pref == 0 && M > 128));
+        p.p256 = ok256 && tile_pref != 128;
         const int64_t tm = p.p256 ? prefill256_tile() : prefill_tile_m();
         const int64_t tn = p.p256 ? prefill256_tile() : prefill_tile_n();
         const int64_t base = ceil_div(M, tm) * ceil_div(N, tn);
