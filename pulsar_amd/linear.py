@@ -1,0 +1,140 @@
+"""W4A16 linear layer: the drop-in for the engine's dense `at::linear` sites.
+
+The reference decode step runs `at::linear(h, W)` on dense bf16/fp16 weights
+for q, k, v, o, gate, up and down (pulsar-core/src/model/qwen3.cpp:82-119,
+qwen2.cpp:78-93).  A `W4A16Linear` holds one such weight in the MARLIN layout
+(int4 words, fp16 or fp32 scales [K/G, N], optional GPTQ zero points and
+act-order permutation) and computes y = x @ W^T (+ bias) through the library's
+GEMM for any leading shape of x, so a model swaps `at::linear(h, W)` for
+`W(h)`.
+
+`W4A16Linear.concat` builds the N-concatenated q|k|v and gate|up linears from
+already repacked members (no requantisation): the MARLIN words are column-block
+major (64-column blocks, each holding all of K), so for members whose N is a
+multiple of 64 the fused weight is their word buffers back to back.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+
+class W4A16Linear(torch.nn.Module):
+    """y = x @ dequant(W)^T (+ bias), W int4 [out_features, in_features] in the MARLIN layout."""
+
+    def __init__(self, weight_marlin: torch.Tensor, scales: torch.Tensor, group_size: int, in_features: int,
+                 out_features: int, qzeros: torch.Tensor | None = None, perm: torch.Tensor | None = None,
+                 bias: torch.Tensor | None = None):
+        super().__init__()
+        k, n, g = int(in_features), int(out_features), int(group_size)
+        if g <= 0 or k % g or k % 8:
+            raise ValueError(f"W4A16Linear: in_features {k} must be a multiple of 8 and of group_size {g}")
+        if tuple(scales.shape) != (k // g, n) or scales.dtype not in (torch.float16, torch.float32):
+            raise ValueError(f"W4A16Linear: scales must be fp16/fp32 [{k // g}, {n}], got {scales.dtype} "
+                             f"{tuple(scales.shape)}")
+        if qzeros is not None and tuple(qzeros.shape) != (k // g, n // 8):
+            raise ValueError(f"W4A16Linear: qzeros must be int32 [{k // g}, {n // 8}]")
+        if perm is not None and perm.numel() == 0:
+            perm = None
+        if perm is not None and tuple(perm.shape) != (k,):
+            raise ValueError(f"W4A16Linear: perm must be int32 [{k}]")
+        if bias is not None and tuple(bias.shape) != (n,):
+            raise ValueError(f"W4A16Linear: bias must be [{n}]")
+        self.in_features, self.out_features, self.group_size = k, n, g
+        self.register_buffer("weight_marlin", weight_marlin)
+        self.register_buffer("scales", scales)
+        self.register_buffer("qzeros", qzeros)
+        self.register_buffer("perm", perm)
+        self.register_buffer("bias", bias)
+
+    # ---- construction from checkpoint tensors -------------------------------------------
+
+    @classmethod
+    def from_packed(cls, weight_packed: torch.Tensor, weight_scale: torch.Tensor, group_size: int,
+                    bias: torch.Tensor | None = None) -> "W4A16Linear":
+        """The reference's quantized weight: `weight_packed` int32 [N, K/8] (nibble k % 8 of word
+        [n, k / 8], two's complement, ops.hpp:148-152) and `weight_scale` [N, K/G]; repacked with
+        repack_w4a16, which keeps the reference's fp32 `scale_marlin` [K/G, N]."""
+        n, k = weight_packed.shape[0], weight_packed.shape[1] * 8
+        wm, sm = ops.repack_w4a16(weight_packed.contiguous(), weight_scale.contiguous(), group_size)
+        return cls(wm, sm, group_size, k, n, bias=bias)
+
+    @classmethod
+    def from_gptq(cls, qweight: torch.Tensor, scales: torch.Tensor, group_size: int,
+                  qzeros: torch.Tensor | None = None, g_idx: torch.Tensor | None = None,
+                  bias: torch.Tensor | None = None) -> "W4A16Linear":
+        """A GPTQ checkpoint's tensors: qweight int32 [K/8, N] (nibble k % 8 = u, unsigned),
+        scales [K/G, N], qzeros int32 [K/G, N/8] holding z itself (convert the original
+        AutoGPTQ "z - 1" storage with `gptq_v1_to_v2_zeros` first), g_idx [K] for act-order.
+        A g_idx equal to k // G is the natural order and needs no permutation."""
+        k, n = qweight.shape[0] * 8, qweight.shape[1]
+        if g_idx is not None:
+            natural = torch.arange(k, device=g_idx.device, dtype=torch.int32) // group_size
+            if torch.equal(g_idx.to(torch.int32), natural):
+                g_idx = None
+        wm, perm = ops.repack_w4a16_gptq(qweight.contiguous(),
+                                         None if g_idx is None else g_idx.to(torch.int32).contiguous(), group_size)
+        sc = scales if scales.dtype in (torch.float16, torch.float32) else scales.float()
+        return cls(wm, sc.contiguous(), group_size, k, n,
+                   qzeros=None if qzeros is None else qzeros.contiguous(),
+                   perm=perm if g_idx is not None else None, bias=bias)
+
+    # ---- compute ------------------------------------------------------------------------
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"W4A16Linear: x has {x.shape[-1]} features, expected {self.in_features}")
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.in_features)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        y = ops.gemm_w4a16_gptq(x2, self.weight_marlin, self.scales, self.qzeros, self.perm, self.group_size)
+        if self.bias is not None:
+            y = y + self.bias.to(y.dtype)
+        return y.reshape(*lead, self.out_features)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, group_size={self.group_size}, "
+                f"zero_points={self.qzeros is not None}, act_order={self.perm is not None}, "
+                f"bias={self.bias is not None}")
+
+    # ---- fusion ---------------------------------------------------------------------------
+
+    @staticmethod
+    def concat(parts: list["W4A16Linear"]) -> "W4A16Linear":
+        """N-concatenation of linears that share their input (q|k|v, gate|up).  Every member but
+        the last needs N % 64 == 0 (no MARLIN padding inside the fused words); all need the same
+        K, group size, scale dtype, zero-point presence and act-order permutation."""
+        if not parts:
+            raise ValueError("W4A16Linear.concat: no parts")
+        if len(parts) == 1:
+            return parts[0]
+        p0 = parts[0]
+        for p in parts:
+            if (p.in_features, p.group_size, p.scales.dtype) != (p0.in_features, p0.group_size, p0.scales.dtype):
+                raise ValueError("W4A16Linear.concat: members differ in K, group size or scale dtype")
+            if (p.qzeros is None) != (p0.qzeros is None) or (p.bias is None) != (p0.bias is None):
+                raise ValueError("W4A16Linear.concat: members differ in zero points or bias")
+            if (p.perm is None) != (p0.perm is None) or (p.perm is not None and not torch.equal(p.perm, p0.perm)):
+                raise ValueError("W4A16Linear.concat: members have different act-order permutations")
+        if any(p.out_features % 64 for p in parts[:-1]):
+            raise ValueError("W4A16Linear.concat: every member but the last needs out_features % 64 == 0")
+        return W4A16Linear(
+            torch.cat([p.weight_marlin for p in parts]),
+            torch.cat([p.scales for p in parts], dim=1),
+            p0.group_size, p0.in_features, sum(p.out_features for p in parts),
+            qzeros=None if p0.qzeros is None else torch.cat([p.qzeros for p in parts], dim=1),
+            perm=p0.perm,
+            bias=None if p0.bias is None else torch.cat([p.bias for p in parts]))
+
+
+def gptq_v1_to_v2_zeros(qzeros: torch.Tensor) -> torch.Tensor:
+    """AutoGPTQ's original checkpoints store each zero point as (z - 1) mod 16 (its kernels add
+    the 1 back); this library's qzeros hold z.  Adds 1 to every nibble, mod 16."""
+    w = qzeros.to(torch.int64) & 0xFFFFFFFF
+    out = torch.zeros_like(w)
+    for i in range(8):
+        out |= (((w >> (4 * i)) + 1) & 0xF) << (4 * i)
+    return out.to(torch.int32)
