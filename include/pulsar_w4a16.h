@@ -125,6 +125,26 @@ int pw4_gemm_w4a16_marlin(const void* x, int x_dtype, const int32_t* weight_marl
                           size_t workspace_bytes, pw4_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * gemm_w4a16_silu_mul: the SwiGLU gate of the MLP in one call,
+ *   y [M, N/2] = silu(x @ Wg^T) * (x @ Wu^T),
+ * replacing the reference's two at::linear calls on gate_proj and up_proj and
+ * the at::silu(gate) * up that follows them (pulsar-core/src/model/qwen3.cpp:
+ * 116-118).  No reference counterpart as one op.  The weight is gate|up
+ * interleaved by 8 columns: fused columns 16j..16j+7 are gate columns
+ * 8j..8j+7 and 16j+8..16j+15 are up columns 8j..8j+7 (N = 2 * intermediate,
+ * N % 16 == 0), in the MARLIN layout; scales, qzeros and perm as for
+ * pw4_gemm_w4a16_marlin, in the same fused column order.  silu and the
+ * product are computed in fp32 on the fp32 GEMM results and rounded once to
+ * x's dtype where the kernel pairs the columns itself (decode without K
+ * slices, the 256-wide prefill kernel, the split-K combine); other plans
+ * round the GEMM output to x's dtype first and gate it in a second pass. */
+size_t pw4_gemm_w4a16_silu_mul_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm);
+int pw4_gemm_w4a16_silu_mul(const void* x, int x_dtype, const int32_t* weight_marlin, const void* scales,
+                            int scale_dtype, const int32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N,
+                            int64_t K, int64_t group_size, void* workspace, size_t workspace_bytes,
+                            pw4_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * GPTQ ingestion (no counterpart in the reference, which has no zero points
  * and no act-order; these follow the public GPTQ checkpoint convention).
  *

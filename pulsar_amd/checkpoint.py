@@ -40,7 +40,7 @@ from dataclasses import dataclass
 
 import torch
 
-from .linear import W4A16Linear, gptq_v1_to_v2_zeros
+from .linear import W4A16Linear, W4A16SiluGate, gptq_v1_to_v2_zeros
 
 PACKED_SUFFIXES = ("weight_packed", "weight_scale", "weight_shape")
 GPTQ_SUFFIXES = ("qweight", "qzeros", "scales", "g_idx")
@@ -180,11 +180,13 @@ def build_linear(fmt: str, parts: dict[str, torch.Tensor], qc: QuantConfig, pref
 
 
 def load_weights(source: str, *, device: torch.device | str, dtype: torch.dtype | None = None,
-                 quant: dict | None = None, fuse: bool = False) -> dict[str, "torch.Tensor | W4A16Linear"]:
+                 quant: dict | None = None, fuse: bool = False,
+                 silu_gate: bool = False) -> dict[str, "torch.Tensor | W4A16Linear"]:
     """Every tensor of the checkpoint at `source`, on `device`; quantized linears come back as
     W4A16Linear under `<prefix>.weight`.  `quant` overrides config.json's quantization_config.
     With `fuse`, q|k|v and gate|up of each layer are N-concatenated into `<layer>.self_attn.
-    qkv_proj.weight` and `<layer>.mlp.gate_up_proj.weight` (the members are dropped)."""
+    qkv_proj.weight` and `<layer>.mlp.gate_up_proj.weight` (the members are dropped); with
+    `silu_gate` as well, the latter is a W4A16SiluGate computing silu(gate) * up."""
     device = torch.device(device)
     cfg = _read_config(source)
     qraw = quant if quant is not None else cfg.get("quantization_config")
@@ -212,14 +214,14 @@ def load_weights(source: str, *, device: torch.device | str, dtype: torch.dtype 
         out[p + ".weight"] = lin
     del tensors
     if fuse:
-        fuse_projections(out)
+        fuse_projections(out, silu_gate=silu_gate)
     return out
 
 
-def fuse_projections(weights: dict) -> None:
+def fuse_projections(weights: dict, silu_gate: bool = False) -> None:
     """In place: `<l>.self_attn.{q,k,v}_proj.weight` -> `<l>.self_attn.qkv_proj.weight` and
-    `<l>.mlp.{gate,up}_proj.weight` -> `<l>.mlp.gate_up_proj.weight`, for every layer whose
-    members are all W4A16Linear (Llama / Qwen naming)."""
+    `<l>.mlp.{gate,up}_proj.weight` -> `<l>.mlp.gate_up_proj.weight` (a W4A16SiluGate with
+    `silu_gate`), for every layer whose members are all W4A16Linear (Llama / Qwen naming)."""
     for key in [k for k in weights if k.endswith(".self_attn.q_proj.weight")]:
         base = key[: -len("q_proj.weight")]
         names = [base + m + "_proj.weight" for m in ("q", "k", "v")]
@@ -229,7 +231,9 @@ def fuse_projections(weights: dict) -> None:
         base = key[: -len("gate_proj.weight")]
         names = [base + m + "_proj.weight" for m in ("gate", "up")]
         if all(isinstance(weights.get(n), W4A16Linear) for n in names):
-            weights[base + "gate_up_proj.weight"] = W4A16Linear.concat([weights.pop(n) for n in names])
+            members = [weights.pop(n) for n in names]
+            weights[base + "gate_up_proj.weight"] = (W4A16SiluGate.from_members(*members) if silu_gate
+                                                     else W4A16Linear.concat(members))
 
 
 def save_archive(path: str, config: dict, tensors: dict[str, torch.Tensor], shards: int = 1) -> None:

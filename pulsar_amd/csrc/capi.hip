@@ -151,18 +151,19 @@ struct Plan {
     int splits = 1;
     size_t partial_bytes = 0;
     size_t xperm_bytes = 0;
+    size_t silu_tmp_bytes = 0;  // SiLU-gated plans whose kernels cannot pair the columns themselves
     // Every non-empty workspace starts with the fixed zero region, so the
     // bytes a decode call uses as counters or exchange slots are never
     // scratch for another call that shares the workspace.
     size_t workspace() const {
-        const size_t rest = align_up(partial_bytes) + align_up(xperm_bytes);
+        const size_t rest = align_up(partial_bytes) + align_up(xperm_bytes) + align_up(silu_tmp_bytes);
         return (rest || tree) ? kZeroRegion + rest : 0;
     }
 };
 
 // layout: LAYOUT_MARLIN or LAYOUT_CT.  num_splits: 0 auto, >= 1 forced.
 Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N, int64_t K, int64_t G, bool has_perm,
-               int64_t num_splits) {
+               int64_t num_splits, bool silu = false) {
     Plan p;
     const int cus = cu_count();
     const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
@@ -334,6 +335,13 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
     // act-order: x is gathered once per call into the workspace, for either
     // kernel (each decode workgroup would otherwise gather the same slice)
     if (has_perm) p.xperm_bytes = (size_t)M * K * 2;
+    // SiLU gating is fused into the decode kernel's direct store, the 256-wide
+    // prefill kernel's unsplit epilogue and the split-K combine; the other
+    // plans (decode K slices, the unsplit 128 x 128 kernel) write the GEMM
+    // output to the workspace and gate it in a second pass
+    if (silu && ((p.decode && (p.tree || p.use_partial)) || (!p.decode && !p.p256 && !p.use_partial))) {
+        p.silu_tmp_bytes = (size_t)M * N * 2;
+    }
     return p;
 }
 
@@ -348,10 +356,11 @@ int check_common(int64_t M, int64_t N, int64_t K, int64_t G, int x_dtype) {
 
 int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const void* scales, int stype,
              const uint32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N, int64_t K, int64_t G,
-             int64_t num_splits, void* workspace, size_t ws_bytes, hipStream_t stream) {
+             int64_t num_splits, void* workspace, size_t ws_bytes, hipStream_t stream, bool silu = false) {
     // x and the weight words are read as 16-byte vectors
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) return PW4_ERR_ARG;
-    const Plan p = make_plan(layout, x_dtype, stype, qzeros != nullptr, M, N, K, G, perm != nullptr, num_splits);
+    const Plan p =
+        make_plan(layout, x_dtype, stype, qzeros != nullptr, M, N, K, G, perm != nullptr, num_splits, silu);
     if (p.workspace() > 0 && (workspace == nullptr || ws_bytes < p.workspace())) return PW4_ERR_WORKSPACE;
     char* ws = reinterpret_cast<char*>(workspace);
     int32_t* counters = p.workspace() ? reinterpret_cast<int32_t*>(ws) : nullptr;
@@ -359,6 +368,11 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
     float* partial = p.partial_bytes ? reinterpret_cast<float*>(ws + kZeroRegion) : nullptr;
     uint16_t* xperm =
         p.xperm_bytes ? reinterpret_cast<uint16_t*>(ws + kZeroRegion + align_up(p.partial_bytes)) : nullptr;
+    uint16_t* silu_tmp = p.silu_tmp_bytes ? reinterpret_cast<uint16_t*>(ws + kZeroRegion + align_up(p.partial_bytes) +
+                                                                        align_up(p.xperm_bytes))
+                                          : nullptr;
+    // the GEMM's own output: y, or the workspace copy a second pass gates into y
+    uint16_t* y_gemm = silu_tmp ? silu_tmp : reinterpret_cast<uint16_t*>(y);
     const int xt = x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16;
     const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
     hipError_t e;
@@ -374,9 +388,10 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.w = w;
         a.scales = scales;
         a.qzeros = qzeros;
-        a.y = reinterpret_cast<uint16_t*>(y);
+        a.y = y_gemm;
         a.partial = p.use_partial ? partial : nullptr;
         a.counters = counters;
+        a.silu = silu && !silu_tmp ? 1 : 0;
         a.slots = slots;
         a.tree_levels = p.tree ? __builtin_ctz((unsigned)p.dc.splits) : 0;
         a.red_single = p.dc.red_single ? 1 : 0;
@@ -406,8 +421,9 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.w = w;
         a.scales = scales;
         a.qzeros = qzeros;
-        a.y = reinterpret_cast<uint16_t*>(y);
+        a.y = y_gemm;
         a.partial = p.use_partial ? partial : nullptr;
+        a.silu = silu && p.p256 && !p.use_partial ? 1 : 0;
         a.M = (int)M;
         a.N = (int)N;
         a.K = (int)K;
@@ -426,7 +442,12 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         if (e != hipSuccess) return hip_fail(e);
     }
     if (p.use_partial && !p.decode) {
-        e = launch_combine(partial, reinterpret_cast<uint16_t*>(y), M * N, p.splits, xt, stream);
+        e = silu ? launch_combine_silu(partial, reinterpret_cast<uint16_t*>(y), M, N, p.splits, xt, stream)
+                 : launch_combine(partial, reinterpret_cast<uint16_t*>(y), M * N, p.splits, xt, stream);
+        if (e != hipSuccess) return hip_fail(e);
+    }
+    if (silu_tmp) {
+        e = launch_silu_mul(silu_tmp, reinterpret_cast<uint16_t*>(y), M, N, xt, stream);
         if (e != hipSuccess) return hip_fail(e);
     }
     return PW4_OK;
@@ -524,6 +545,29 @@ int pw4_gemm_w4a16_marlin(const void* x, int x_dtype, const int32_t* weight_marl
                     scale_dtype == PW4_DTYPE_F32 ? S_F32 : S_F16, reinterpret_cast<const uint32_t*>(qzeros), perm, y,
                     M, N, K, group_size, num_splits, workspace, workspace_bytes,
                     reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t pw4_gemm_w4a16_silu_mul_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm) {
+    if (check_common(M, N, K, group_size, PW4_DTYPE_F16) != PW4_OK || M == 0 || N == 0 || N % 16 != 0) return 0;
+    return std::max(
+        make_plan(LAYOUT_MARLIN, PW4_DTYPE_F16, S_F16, true, M, N, K, group_size, has_perm != 0, 0, true).workspace(),
+        make_plan(LAYOUT_MARLIN, PW4_DTYPE_BF16, S_F16, true, M, N, K, group_size, has_perm != 0, 0, true).workspace());
+}
+
+int pw4_gemm_w4a16_silu_mul(const void* x, int x_dtype, const int32_t* weight_marlin, const void* scales,
+                            int scale_dtype, const int32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N,
+                            int64_t K, int64_t group_size, void* workspace, size_t workspace_bytes,
+                            pw4_stream_t stream) {
+    int rc = check_common(M, N, K, group_size, x_dtype);
+    if (rc != PW4_OK) return rc;
+    if (scale_dtype != PW4_DTYPE_F32 && scale_dtype != PW4_DTYPE_F16) return PW4_ERR_ARG;
+    if (N % 16 != 0) return PW4_ERR_SHAPE;  // whole gate|up strips of 8 + 8 columns
+    if (M == 0 || N == 0) return PW4_OK;
+    if (!x || !weight_marlin || !scales || !y) return PW4_ERR_ARG;
+    return run_gemm(LAYOUT_MARLIN, x, x_dtype, reinterpret_cast<const uint32_t*>(weight_marlin), scales,
+                    scale_dtype == PW4_DTYPE_F32 ? S_F32 : S_F16, reinterpret_cast<const uint32_t*>(qzeros), perm, y,
+                    M, N, K, group_size, 0, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream),
+                    /*silu=*/true);
 }
 
 int pw4_gidx_to_perm(const int32_t* g_idx, int64_t K, int64_t group_size, int32_t* perm, int32_t* status_dev,

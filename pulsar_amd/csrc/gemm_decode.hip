@@ -516,6 +516,18 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
             return;
         }
         if (a.partial == nullptr) {
+            if (a.silu) {
+                // gate|up pairs: column c and c + 8 of each 16-column strip
+                const int nh = N >> 1;
+                for (int j = tid; j < nout / 2; j += kThreads) {
+                    const int i = ((j >> 3) << 4) | (j & 7);  // gate element of pair j
+                    const int row = i >> (4 + cwn_log2), c = i & (nb - 1);
+                    const int n = ((col0 + c) >> 4 << 3) | (c & 7);  // output column: strip * 8 + c % 8
+                    const float v = silu_mul(reduced(i), reduced(i + 8));
+                    if (col0 + c < N) a.y[(int64_t)row * nh + n] = f32_to_out<BF16>(v);
+                }
+                return;
+            }
             for (int i = tid; i < nout; i += kThreads) {
                 const int row = i >> (4 + cwn_log2), n = col0 + (i & (nb - 1));
                 const float v = reduced(i);
@@ -662,6 +674,41 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     }
 }
 
+// Output element o of y [M, N/2]: row o / (N/2); strip (o % (N/2)) / 8 holds
+// the gate column strip * 16 + o % 8 and the up column 8 further.
+__device__ __forceinline__ int64_t silu_gate_index(int64_t o, int64_t nh) {
+    const int64_t row = o / nh, oc = o - row * nh;
+    return row * (2 * nh) + ((oc >> 3) << 4) + (oc & 7);
+}
+
+// Fixed-order sum of gate|up interleaved [splits, M, N] fp32 partials, then
+// silu(gate) * up in fp32 and the cast to y [M, N/2]: the split-K combine of a
+// SiLU-gated GEMM.
+template <bool BF16>
+__global__ __launch_bounds__(256) void combine_silu_kernel(const float* __restrict__ partial, uint16_t* __restrict__ y,
+                                                           int64_t mn, int64_t nh, int splits) {
+    const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (o >= mn / 2) return;
+    const int64_t gi = silu_gate_index(o, nh);
+    float g = 0.f, u = 0.f;
+    for (int k = 0; k < splits; ++k) {
+        g += partial[(int64_t)k * mn + gi];
+        u += partial[(int64_t)k * mn + gi + 8];
+    }
+    y[o] = f32_to_out<BF16>(silu_mul(g, u));
+}
+
+// y [M, N/2] = silu(gate) * up from a finished GEMM output h [M, N] (gate|up
+// interleaved by 8), for plans whose GEMM cannot pair the columns itself.
+template <bool BF16>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ h, uint16_t* __restrict__ y,
+                                                       int64_t total, int64_t nh) {
+    const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (o >= total) return;
+    const int64_t gi = silu_gate_index(o, nh);
+    y[o] = f32_to_out<BF16>(silu_mul(half_to_f32<BF16>(h[gi]), half_to_f32<BF16>(h[gi + 8])));
+}
+
 }  // namespace
 
 size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single) {
@@ -709,6 +756,33 @@ hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const Decode
     hipError_t e = prepare(fn, cfg.lds_bytes);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(fn, dim3(a.wps, a.splits), dim3(kThreads), cfg.lds_bytes, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine_silu(const float* partial, uint16_t* y, int64_t M, int64_t N, int splits, int xtype,
+                               hipStream_t stream) {
+    if (N % 16 != 0) return hipErrorInvalidValue;
+    const int64_t blocks = ceil_div(M * N / 2, 256);
+    if (blocks == 0) return hipSuccess;
+    if (xtype == X_BF16) {
+        hipLaunchKernelGGL(combine_silu_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, partial, y, M * N,
+                           N / 2, splits);
+    } else {
+        hipLaunchKernelGGL(combine_silu_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, partial, y, M * N,
+                           N / 2, splits);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const uint16_t* h, uint16_t* y, int64_t M, int64_t N, int xtype, hipStream_t stream) {
+    if (N % 16 != 0) return hipErrorInvalidValue;
+    const int64_t blocks = ceil_div(M * N / 2, 256);
+    if (blocks == 0) return hipSuccess;
+    if (xtype == X_BF16) {
+        hipLaunchKernelGGL(silu_mul_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, h, y, M * N / 2, N / 2);
+    } else {
+        hipLaunchKernelGGL(silu_mul_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, h, y, M * N / 2, N / 2);
+    }
     return hipGetLastError();
 }
 

@@ -264,6 +264,33 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
     // whose column is past N start at 2 GiB, beyond the range.
     const int rows = min(M - m0, TMR);
     if constexpr (!PARTIAL) {
+        if (a.silu) {
+            // gate|up interleaved by 8: a gate lane (column c % 16 < 8) takes its
+            // up value from lane ^ 8 (column c + 8, same rows) and stores
+            // silu(gate) * up into y [M, N/2]; up lanes store nothing
+            const int nh = N >> 1;
+            const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(a.y + (int64_t)m0 * nh, (short)0,
+                                                                                rows * nh * 2, 0x00020000);
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const int n = ncol0 + ct * 32 + c;
+                const int on = (n >> 4 << 3) | (n & 7);
+                const uint32_t base = (n < N && (c & 8) == 0) ? (uint32_t)(4 * hb * nh + on) * 2u : 0x80000000u;
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int r = rt * 32 + 8 * (e >> 2) + (e & 3);
+                        const float g = acc[rt][ct][e];
+                        const float u = __shfl_xor(g, 8);
+                        const uint32_t off = base + (uint32_t)(r * nh * 2);
+                        __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<false>(silu_mul(g, u)), out, (int)off, 0, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            return;
+        }
         const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(a.y + (int64_t)m0 * N, (short)0,
                                                                             rows * N * 2, 0x00020000);
 #pragma unroll

@@ -94,7 +94,8 @@ at::Tensor gemm_w4a16_run(const at::Tensor& x, const at::Tensor& weight_packed, 
 
 at::Tensor marlin_run(const at::Tensor& x, const at::Tensor& weight_marlin, const at::Tensor& scales,
                       const std::optional<at::Tensor>& qzeros, const std::optional<at::Tensor>& perm,
-                      int64_t group_size, int64_t forced_splits, const char* op, bool fp32_scales_only) {
+                      int64_t group_size, int64_t forced_splits, const char* op, bool fp32_scales_only,
+                      bool silu = false) {
     TORCH_CHECK(x.is_cuda() && weight_marlin.is_cuda() && scales.is_cuda(), op, ": all inputs must be CUDA tensors");
     TORCH_CHECK(x.scalar_type() == at::kHalf || x.scalar_type() == at::kBFloat16, op, ": x must be fp16 or bf16");
     TORCH_CHECK(weight_marlin.scalar_type() == at::kInt, op, ": weight_marlin must be int32");
@@ -132,6 +133,19 @@ at::Tensor marlin_run(const at::Tensor& x, const at::Tensor& weight_marlin, cons
     DeviceGuard guard(x.device());
     auto wm = weight_marlin.contiguous();
     auto sm = scales.contiguous();
+    if (silu) {
+        TORCH_CHECK(N % 16 == 0, op, ": N (gate|up interleaved by 8) must be a multiple of 16");
+        auto y = at::empty({M, N / 2}, x.options());
+        if (M == 0 || N == 0) return y;
+        const size_t wsb = pw4_gemm_w4a16_silu_mul_workspace_size(M, N, K, group_size, pp != nullptr);
+        at::Tensor wsp = workspace(wsb, x);
+        const int rc = pw4_gemm_w4a16_silu_mul(x.data_ptr(), x_dtype_code(x), wm.data_ptr<int32_t>(), sm.data_ptr(),
+                                               sm.scalar_type() == at::kFloat ? PW4_DTYPE_F32 : PW4_DTYPE_F16, zp, pp,
+                                               y.data_ptr(), M, N, K, group_size, ptr_or_null(wsp), wsb,
+                                               current_stream());
+        check_status(rc, op);
+        return y;
+    }
     auto y = at::empty({M, N}, x.options());
     if (M == 0 || N == 0) return y;
     const size_t wsb = pw4_gemm_w4a16_marlin_workspace_size(M, N, K, group_size, pp != nullptr, forced_splits);
@@ -236,6 +250,14 @@ at::Tensor gemm_w4a16_gptq_cuda(const at::Tensor& x, const at::Tensor& weight_ma
     return marlin_run(x, weight_marlin, scales, qzeros, perm, group_size, 0, "gemm_w4a16_gptq", false);
 }
 
+// silu(x @ Wg^T) * (x @ Wu^T) from a gate|up weight interleaved by 8 columns:
+// the MLP gate of qwen3.cpp:116-118 in one op.
+at::Tensor gemm_w4a16_silu_mul_cuda(const at::Tensor& x, const at::Tensor& weight_marlin, const at::Tensor& scales,
+                                    const std::optional<at::Tensor>& qzeros, const std::optional<at::Tensor>& perm,
+                                    int64_t group_size) {
+    return marlin_run(x, weight_marlin, scales, qzeros, perm, group_size, 0, "gemm_w4a16_silu_mul", false, true);
+}
+
 }  // namespace pulsar
 
 // Schema strings: the first four are the reference ABI verbatim.
@@ -253,6 +275,9 @@ TORCH_LIBRARY_FRAGMENT(pulsar, m) {
     m.def(
         "gemm_w4a16_gptq(Tensor x, Tensor weight_marlin, Tensor scales, Tensor? qzeros, Tensor? perm, "
         "int group_size) -> Tensor");
+    m.def(
+        "gemm_w4a16_silu_mul(Tensor x, Tensor weight_marlin, Tensor scales, Tensor? qzeros, Tensor? perm, "
+        "int group_size) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(pulsar, CUDA, m) {
@@ -263,4 +288,5 @@ TORCH_LIBRARY_IMPL(pulsar, CUDA, m) {
     m.impl("gemm_w4a16_marlin_split", TORCH_FN(pulsar::gemm_w4a16_marlin_split_cuda));
     m.impl("repack_w4a16_gptq", TORCH_FN(pulsar::repack_w4a16_gptq_cuda));
     m.impl("gemm_w4a16_gptq", TORCH_FN(pulsar::gemm_w4a16_gptq_cuda));
+    m.impl("gemm_w4a16_silu_mul", TORCH_FN(pulsar::gemm_w4a16_silu_mul_cuda));
 }

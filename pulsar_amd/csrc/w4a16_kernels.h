@@ -48,6 +48,10 @@ struct DecodeArgs {
     int k_per_split;         // multiple of 128
     int rowstride;           // LDS row stride of the staged x, in halves (k_per_split + 8)
     int splits;
+    // SiLU-gated output (direct store only): the columns are gate|up
+    // interleaved by 8 (fused columns 16j..16j+7 gate, 16j+8..16j+15 up) and
+    // y is [M, N/2] = silu(gate) * up
+    int silu;
     NibbleMasks masks;
 };
 
@@ -78,6 +82,13 @@ int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          hipStream_t stream);
 hipError_t launch_combine(const float* partial, uint16_t* y, int64_t mn, int splits, int xtype, hipStream_t stream);
+// The same fixed-order sum over [splits, M, N] partials of gate|up interleaved
+// columns (N % 16 == 0), writing y [M, N/2] = silu(gate) * up.
+hipError_t launch_combine_silu(const float* partial, uint16_t* y, int64_t M, int64_t N, int splits, int xtype,
+                               hipStream_t stream);
+// y [M, N/2] = silu(gate) * up from a GEMM output h [M, N] in the same
+// interleaved column order, h and y in x's dtype.
+hipError_t launch_silu_mul(const uint16_t* h, uint16_t* y, int64_t M, int64_t N, int xtype, hipStream_t stream);
 
 // Prefill GEMM (large M): 128 x 128 output tile per workgroup, BK = 64.
 struct PrefillArgs {
@@ -95,6 +106,7 @@ struct PrefillArgs {
     int n_begin, n_end;      // output columns a launch covers (set by the 256-tile launcher)
     int cus;                 // compute units of the device (tail balancing)
     int tile_rows;           // 256-wide kernel: 256-row tiles (tail balanced when unsplit) or 128-row tiles
+    int silu;                // 256-wide kernel, unsplit: y [M, N/2] = silu(gate) * up (see DecodeArgs)
 };
 
 hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream);

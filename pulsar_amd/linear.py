@@ -95,6 +95,17 @@ class W4A16Linear(torch.nn.Module):
             y = y + self.bias.to(y.dtype)
         return y.reshape(*lead, self.out_features)
 
+    def bytes_per_call(self, m: int) -> int:
+        """Algorithmic HBM bytes of one call at batch m: int4 weights, scales, zero points,
+        permutation, x and y."""
+        k, n, kg = self.in_features, self.out_features, self.in_features // self.group_size
+        b = n * k // 2 + n * kg * self.scales.element_size() + m * k * 2 + m * n * 2
+        if self.qzeros is not None:
+            b += n * kg // 2
+        if self.perm is not None:
+            b += k * 4
+        return b
+
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, group_size={self.group_size}, "
                 f"zero_points={self.qzeros is not None}, act_order={self.perm is not None}, "
@@ -138,3 +149,61 @@ def gptq_v1_to_v2_zeros(qzeros: torch.Tensor) -> torch.Tensor:
     for i in range(8):
         out |= (((w >> (4 * i)) + 1) & 0xF) << (4 * i)
     return out.to(torch.int32)
+
+
+def _groups8(words: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """MARLIN words of an [n, k] weight as its 8-column groups: [n/8, Kpad/64, 2, 32] (a
+    64-column block's chunk half holds 8 groups of 8 columns, 32 words each)."""
+    ncb, nch = n // 64, -(-k // 64)
+    return words.view(ncb, nch, 2, 8, 32).permute(0, 3, 1, 2, 4).reshape(ncb * 8, nch, 2, 32)
+
+
+class W4A16SiluGate(W4A16Linear):
+    """The SwiGLU gate of an MLP in one GEMM: y = silu(x @ Wg^T) * (x @ Wu^T), [..., F].
+
+    Holds gate and up as one weight of 2F columns interleaved by 8 (fused columns 16j..16j+7
+    are gate 8j..8j+7, 16j+8..16j+15 are up 8j..8j+7), so every 16-column strip the kernels
+    finish together carries matching gate and up columns; the reference runs two at::linear
+    calls and at::silu(gate) * up (pulsar-core/src/model/qwen3.cpp:116-118)."""
+
+    @classmethod
+    def from_members(cls, gate: W4A16Linear, up: W4A16Linear) -> "W4A16SiluGate":
+        """Interleave two repacked linears (same K, group size, scale dtype, zero points and
+        act-order; F % 64 == 0) by regrouping their MARLIN words: no requantisation."""
+        f, k = gate.out_features, gate.in_features
+        if (up.out_features, up.in_features, up.group_size, up.scales.dtype) != \
+                (f, k, gate.group_size, gate.scales.dtype):
+            raise ValueError("W4A16SiluGate: gate and up differ in shape, group size or scale dtype")
+        if f % 64:
+            raise ValueError("W4A16SiluGate: the intermediate size must be a multiple of 64")
+        if (gate.qzeros is None) != (up.qzeros is None) or (gate.bias is not None or up.bias is not None):
+            raise ValueError("W4A16SiluGate: zero points must match; biases are not supported")
+        if (gate.perm is None) != (up.perm is None) or (gate.perm is not None and not torch.equal(gate.perm, up.perm)):
+            raise ValueError("W4A16SiluGate: gate and up have different act-order permutations")
+        nch = -(-k // 64)
+        groups = torch.stack([_groups8(gate.weight_marlin, f, k), _groups8(up.weight_marlin, f, k)], dim=1)
+        words = groups.reshape(2 * f // 64, 8, nch, 2, 32).permute(0, 2, 3, 1, 4).reshape(-1).contiguous()
+        kg = k // gate.group_size
+
+        def inter(a: torch.Tensor, b: torch.Tensor, width: int) -> torch.Tensor:
+            return torch.stack([a.view(kg, -1, width), b.view(kg, -1, width)], dim=2).reshape(kg, -1).contiguous()
+
+        return cls(words, inter(gate.scales, up.scales, 8), gate.group_size, k, 2 * f,
+                   qzeros=None if gate.qzeros is None else inter(gate.qzeros, up.qzeros, 1), perm=gate.perm)
+
+    @property
+    def intermediate(self) -> int:
+        return self.out_features // 2
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"W4A16SiluGate: x has {x.shape[-1]} features, expected {self.in_features}")
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.in_features)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        y = ops.gemm_w4a16_silu_mul(x2, self.weight_marlin, self.scales, self.qzeros, self.perm, self.group_size)
+        return y.reshape(*lead, self.intermediate)
+
+    def bytes_per_call(self, m: int) -> int:
+        return super().bytes_per_call(m) - m * self.intermediate * 2

@@ -55,6 +55,10 @@ def _gemm_w4a16_gptq_fake(x, weight_marlin, scales, qzeros, perm, group_size):
     return x.new_empty((x.shape[0], scales.shape[1]))
 
 
+def _gemm_w4a16_silu_mul_fake(x, weight_marlin, scales, qzeros, perm, group_size):
+    return x.new_empty((x.shape[0], scales.shape[1] // 2))
+
+
 def _register_fakes() -> None:
     fakes = {
         "pulsar::gemm_w4a16": _gemm_w4a16_fake,
@@ -64,6 +68,7 @@ def _register_fakes() -> None:
         "pulsar::gemm_w4a16_marlin_split": _gemm_w4a16_marlin_split_fake,
         "pulsar::repack_w4a16_gptq": _repack_w4a16_gptq_fake,
         "pulsar::gemm_w4a16_gptq": _gemm_w4a16_gptq_fake,
+        "pulsar::gemm_w4a16_silu_mul": _gemm_w4a16_silu_mul_fake,
     }
     for name, func in fakes.items():
         torch.library.register_fake(name, func)
@@ -132,3 +137,13 @@ def gemm_w4a16_gptq(x: torch.Tensor, weight_marlin: torch.Tensor, scales: torch.
     if perm is not None and perm.numel() == 0:
         perm = None
     return torch.ops.pulsar.gemm_w4a16_gptq(x, weight_marlin, scales, qzeros, perm, group_size)
+
+
+def gemm_w4a16_silu_mul(x: torch.Tensor, weight_marlin: torch.Tensor, scales: torch.Tensor,
+                        qzeros: torch.Tensor | None, perm: torch.Tensor | None, group_size: int) -> torch.Tensor:
+    """silu(x @ Wg^T) * (x @ Wu^T), [M, N/2], from a gate|up weight interleaved by 8 columns
+    (fused columns 16j..16j+7 gate 8j..8j+7, 16j+8..16j+15 up 8j..8j+7): the reference MLP's
+    at::silu(gate) * up after two at::linear calls (qwen3.cpp:116-118) as one op."""
+    if perm is not None and perm.numel() == 0:
+        perm = None
+    return torch.ops.pulsar.gemm_w4a16_silu_mul(x, weight_marlin, scales, qzeros, perm, group_size)

@@ -17,16 +17,14 @@ the model.
 
 The reference has no such runner (its engine calls bf16 at::linear at
 pulsar-core/src/models/qwen3.cpp:82-119); this is the drop-in's counterpart of
-that decode step's linear layers, built on the ops in pulsar_amd.ops.
+that decode step's linear layers, built on W4A16Linear (pulsar_amd.linear).
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass
-
 import torch
 
-from . import ops
+from .linear import W4A16Linear
 
 # (name, K, N) of the seven linears of one Llama-3-8B layer (hidden 4096, 8 KV
 # heads of 128, MLP 14336).
@@ -46,58 +44,55 @@ LLAMA3_8B_LINEARS = (
 LLAMA3_8B_FUSED = (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",)))
 
 
-@dataclass
-class QuantLinear:
-    """One linear in the MARLIN layout: weight_marlin int32 words, fp16 scales [K/G, N]."""
-
-    name: str
-    k: int
-    n: int
-    weight_marlin: torch.Tensor
-    scales: torch.Tensor
-
-    def bytes_per_call(self, m: int, group_size: int) -> int:
-        """Algorithmic HBM bytes of one call: int4 weights, fp16 scales, x, y."""
-        return self.n * self.k // 2 + self.n * (self.k // group_size) * 2 + m * self.k * 2 + m * self.n * 2
-
-
 def random_layers(num_layers: int, shapes=LLAMA3_8B_LINEARS, group_size: int = 128, device="cuda:0",
-                  seed: int = 0) -> list[list[QuantLinear]]:
-    """Random symmetric int4 weights (u ~ U{0..15}, zero 8) and |N(0, 0.02)| + 1e-3
-    fp16 scales, generated on the device and repacked to the MARLIN layout."""
+                  seed: int = 0, stats: dict | None = None) -> list[list[W4A16Linear]]:
+    """Random symmetric int4 GPTQ weights (u ~ U{0..15}, zero 8) and |N(0, 0.02)| + 1e-3 fp16
+    scales, generated on the device and repacked to the MARLIN layout, as a checkpoint load
+    would.  With `stats`, the repack time and bytes (qweight read, MARLIN words written) are
+    accumulated into stats["repack_ms"] and stats["repack_bytes"]."""
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
+    events = []
+    nbytes = 0
     layers = []
     for _ in range(num_layers):
         layer = []
         for name, k, n in shapes:
             qweight = torch.randint(-(2 ** 31), 2 ** 31, (k // 8, n), dtype=torch.int32, device=device,
                                     generator=gen)
-            wm, _ = ops.repack_w4a16_gptq(qweight, None, group_size)
-            del qweight
             scales = (torch.randn(k // group_size, n, device=device, generator=gen) * 0.02).abs_().add_(1e-3).half()
-            layer.append(QuantLinear(name, k, n, wm, scales))
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) if stats is not None \
+                else None
+            if ev:
+                ev[0].record()
+            lin = W4A16Linear.from_gptq(qweight, scales, group_size)
+            if ev:
+                ev[1].record()
+                events.append(ev)
+                nbytes += qweight.numel() * 4 + lin.weight_marlin.numel() * 4
+            lin.name = name
+            layer.append(lin)
+            del qweight
         layers.append(layer)
+    if stats is not None:
+        torch.cuda.synchronize()
+        stats["repack_ms"] = stats.get("repack_ms", 0.0) + sum(a.elapsed_time(b) for a, b in events)
+        stats["repack_bytes"] = stats.get("repack_bytes", 0) + nbytes
     return layers
 
 
-def fuse_layers(layers: list[list[QuantLinear]], groups=LLAMA3_8B_FUSED) -> list[list[QuantLinear]]:
-    """N-concatenate linears that share their input.  The MARLIN word order is
-    column-block major (64-column blocks, each holding all of K), so for
-    members whose N is a multiple of 64 the fused weight is the members'
-    weight buffers back to back; the scales concatenate along N."""
+def fuse_layers(layers: list[list[W4A16Linear]], groups=LLAMA3_8B_FUSED) -> list[list[W4A16Linear]]:
+    """N-concatenate linears that share their input (W4A16Linear.concat: the members' MARLIN
+    words back to back, their scales along N)."""
     fused = []
     for layer in layers:
         by_name = {lin.name: lin for lin in layer}
         out = []
         for name, members in groups:
-            parts = [by_name[m] for m in members]
-            k = parts[0].k
-            if any(p.k != k for p in parts) or any(p.n % 64 for p in parts[:-1]):
-                raise ValueError(f"cannot fuse {members}: K differs or N not a multiple of 64")
-            wm = torch.cat([p.weight_marlin for p in parts]) if len(parts) > 1 else parts[0].weight_marlin
-            sc = torch.cat([p.scales for p in parts], dim=1) if len(parts) > 1 else parts[0].scales
-            out.append(QuantLinear(name, k, sum(p.n for p in parts), wm, sc))
+            lin = W4A16Linear.concat([by_name[m] for m in members])
+            if len(members) > 1:
+                lin.name = name
+            out.append(lin)
         fused.append(out)
     return fused
 
@@ -112,7 +107,7 @@ class W4A16LinearStack:
     may overwrite between steps.
     """
 
-    def __init__(self, layers: list[list[QuantLinear]], m: int, group_size: int = 128, device="cuda:0",
+    def __init__(self, layers: list[list[W4A16Linear]], m: int, group_size: int = 128, device="cuda:0",
                  seed: int = 1):
         self.layers = layers
         self.m = m
@@ -120,22 +115,14 @@ class W4A16LinearStack:
         self.device = torch.device(device)
         gen = torch.Generator(device=self.device)
         gen.manual_seed(seed)
-        ks = sorted({lin.k for layer in layers for lin in layer})
+        ks = sorted({lin.in_features for layer in layers for lin in layer})
         self.inputs = {k: torch.randn(m, k, device=self.device, generator=gen).half() for k in ks}
         self.graph: torch.cuda.CUDAGraph | None = None
         self.outputs: list[torch.Tensor] = []
         self.stream = torch.cuda.Stream(device=self.device)
 
-    def _input_for(self, lin: QuantLinear) -> torch.Tensor:
-        return self.inputs[lin.k]
-
     def forward(self) -> list[torch.Tensor]:
-        outs = []
-        for layer in self.layers:
-            for lin in layer:
-                outs.append(ops.gemm_w4a16_gptq(self._input_for(lin), lin.weight_marlin, lin.scales, None, None,
-                                                self.group_size))
-        return outs
+        return [lin(self.inputs[lin.in_features]) for layer in self.layers for lin in layer]
 
     def capture(self) -> None:
         # One eager pass on the capture stream first: it sizes the shared
@@ -153,7 +140,7 @@ class W4A16LinearStack:
         self.graph.replay()
 
     def bytes_per_step(self) -> int:
-        return sum(lin.bytes_per_call(self.m, self.group_size) for layer in self.layers for lin in layer)
+        return sum(lin.bytes_per_call(self.m) for layer in self.layers for lin in layer)
 
     def launches_per_step(self) -> int:
         return sum(len(layer) for layer in self.layers)

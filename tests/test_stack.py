@@ -12,7 +12,8 @@ import torch
 
 from oracle import oracle as O
 from pulsar_amd import ops
-from pulsar_amd.stack import LLAMA3_8B_LINEARS, QuantLinear, W4A16LinearStack, fuse_layers, random_layers
+from pulsar_amd.linear import W4A16Linear
+from pulsar_amd.stack import LLAMA3_8B_LINEARS, W4A16LinearStack, fuse_layers, random_layers
 from w4a16_case import check, to_device_x
 
 pytestmark = pytest.mark.gpu
@@ -48,7 +49,9 @@ def test_stack_graph_matches_oracle(m):
         qweight = torch.from_numpy(O.pack_gptq(p.u)).cuda()
         wm, _ = ops.repack_w4a16_gptq(qweight, None, G)
         scales = torch.from_numpy(p.scale_kn).half().cuda()  # exact: the values are fp16
-        layer.append(QuantLinear(name, k, p.n, wm, scales))
+        lin = W4A16Linear(wm, scales, G, k, p.n)
+        lin.name = name
+        layer.append(lin)
     st = W4A16LinearStack([layer], m)
     for k, p in probs.items():
         st.inputs[k].copy_(to_device_x(p.x16, torch.float16))
@@ -77,7 +80,7 @@ def test_fused_stack_equals_unfused(m):
     where they do not."""
     layers = random_layers(1, device="cuda:0", seed=5)
     fused = fuse_layers(layers)
-    assert [(l.name, l.k, l.n) for l in fused[0]] == [("qkv", 4096, 6144), ("o", 4096, 4096),
+    assert [(l.name, l.in_features, l.out_features) for l in fused[0]] == [("qkv", 4096, 6144), ("o", 4096, 4096),
                                                       ("gate_up", 4096, 28672), ("down", 14336, 4096)]
     a = W4A16LinearStack(layers, m, seed=7)
     b = W4A16LinearStack(fused, m, seed=7)
