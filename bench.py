@@ -222,13 +222,24 @@ def stack_bench(torch, dev, steps: int, warmup: int) -> dict:
     """Config 5: the 32-layer linear stack as one graph per step, M = 1 and 32."""
     from pulsar_amd.stack import W4A16LinearStack, fuse_layers, random_layers
 
-    layers = random_layers(STACK_LAYERS, device=dev, seed=0)
+    rep: dict = {}
+    layers = random_layers(STACK_LAYERS, device=dev, seed=0, stats=rep)
     out = {"layers": STACK_LAYERS, "linears_per_layer": len(layers[0]),
+           "repack_at_load": {"linears": STACK_LAYERS * len(layers[0]), "ms": round(rep["repack_ms"], 2),
+                              "bytes": rep["repack_bytes"],
+                              "GB/s": round(rep["repack_bytes"] / (rep["repack_ms"] * 1e-3) / 1e9, 1),
+                              "note": "GPTQ qweight -> MARLIN words, qweight read + words written, per-linear "
+                                      "HIP events"},
            "weight_bytes": sum(l.weight_marlin.numel() * 4 + l.scales.numel() * 2 for ly in layers for l in ly),
            "note": "m1/m32: the 7 linears per layer as 7 launches; fused_m1/fused_m32: q|k|v and gate|up "
-                   "N-concatenated (4 launches per layer, same weights and outputs)"}
+                   "N-concatenated (4 launches per layer, same weights and outputs); gated_m1/gated_m32: "
+                   "q|k|v fused and gate|up as one SiLU-gated GEMM whose silu(gate)*up output feeds down, "
+                   "the model's MLP (4 launches per layer, no separate activation kernel)"}
     fused = fuse_layers(layers)
-    for tag, ls, m in [(f"m{m}", layers, m) for m in STACK_M] + [(f"fused_m{m}", fused, m) for m in STACK_M]:
+    gated = fuse_layers(layers, silu_gate=True)
+    runs = ([(f"m{m}", layers, m) for m in STACK_M] + [(f"fused_m{m}", fused, m) for m in STACK_M] +
+            [(f"gated_m{m}", gated, m) for m in STACK_M])
+    for tag, ls, m in runs:
         st = W4A16LinearStack(ls, m, device=dev)
         st.capture()
         for _ in range(warmup):
@@ -248,7 +259,7 @@ def stack_bench(torch, dev, steps: int, warmup: int) -> dict:
                         "launches": st.launches_per_step(), "bytes_per_step": st.bytes_per_step(),
                         "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
         del st
-    del layers, fused
+    del layers, fused, gated
     torch.cuda.empty_cache()
     return out
 

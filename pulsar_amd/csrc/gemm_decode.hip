@@ -517,14 +517,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
         }
         if (a.partial == nullptr) {
             if (a.silu) {
-                // gate|up pairs: column c and c + 8 of each 16-column strip
+                // gate|up pairs: column c and c + 8 of each 16-column strip,
+                // elements i and i ^ 8, held by lanes tid and tid ^ 8 of one
+                // wave (nout is a multiple of 16, so both run the same trips)
                 const int nh = N >> 1;
-                for (int j = tid; j < nout / 2; j += kThreads) {
-                    const int i = ((j >> 3) << 4) | (j & 7);  // gate element of pair j
+                for (int i = tid; i < nout; i += kThreads) {
                     const int row = i >> (4 + cwn_log2), c = i & (nb - 1);
+                    const float v = reduced(i);
+                    const float up = __shfl_xor(v, 8);
                     const int n = ((col0 + c) >> 4 << 3) | (c & 7);  // output column: strip * 8 + c % 8
-                    const float v = silu_mul(reduced(i), reduced(i + 8));
-                    if (col0 + c < N) a.y[(int64_t)row * nh + n] = f32_to_out<BF16>(v);
+                    if ((c & 8) == 0 && col0 + c < N) a.y[(int64_t)row * nh + n] = f32_to_out<BF16>(silu_mul(v, up));
                 }
                 return;
             }

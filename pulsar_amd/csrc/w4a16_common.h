@@ -194,12 +194,13 @@ __device__ __forceinline__ float load_scale(const T* p) {
 }
 
 // silu(g) * u in fp32: g * u / (1 + e^-g), e^-g as 2^(-g log2 e) on the
-// hardware exp2.  For g below about -88 the exponential overflows to +inf and
-// the product is -0 (the limit), for g above about 88 it is 0 and the result
-// is g * u.
+// hardware exp2 and the quotient through the hardware reciprocal (1 ulp; the
+// result is rounded to 16 bits).  For g below about -88 the exponential
+// overflows to +inf and the product is -0 (the limit), for g above about 88 it
+// is 0 and the result is g * u.
 __device__ __forceinline__ float silu_mul(float g, float u) {
     const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
-    return g * u / (1.0f + e);
+    return g * u * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 template <bool BF16>

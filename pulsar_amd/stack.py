@@ -8,12 +8,14 @@ every linear of every layer into one graph for a fixed batch M, and replays it
 per step, so the per-token cost is the kernels' own HBM time with no host
 launch gaps.
 
-Activations are not chained through the layers: the attention and MLP maths
-between the linears is outside this path, and chaining raw GEMM outputs would
-grow the values by ~6x per GEMM until fp16 overflows.  Every linear reads a
-fixed input of its K (x_attn [M, 4096] for q/k/v/o/gate/up, x_mlp [M, 14336]
+Activations are not chained from layer to layer: the attention and norm
+maths between the linears is outside this path, and chaining raw GEMM outputs
+would grow the values by ~6x per GEMM until fp16 overflows.  Every linear reads
+a fixed input of its K (x_attn [M, 4096] for q/k/v/o/gate/up, x_mlp [M, 14336]
 for down), which leaves each kernel's work and traffic exactly what it is in
-the model.
+the model.  The one exception is the MLP with its gate fused
+(`fuse_layers(..., silu_gate=True)`): there down reads the W4A16SiluGate's
+output silu(gate) * up, exactly as in the model.
 
 The reference has no such runner (its engine calls bf16 at::linear at
 pulsar-core/src/models/qwen3.cpp:82-119); this is the drop-in's counterpart of
@@ -24,7 +26,7 @@ from __future__ import annotations
 
 import torch
 
-from .linear import W4A16Linear
+from .linear import W4A16Linear, W4A16SiluGate
 
 # (name, K, N) of the seven linears of one Llama-3-8B layer (hidden 4096, 8 KV
 # heads of 128, MLP 14336).
@@ -81,15 +83,21 @@ def random_layers(num_layers: int, shapes=LLAMA3_8B_LINEARS, group_size: int = 1
     return layers
 
 
-def fuse_layers(layers: list[list[W4A16Linear]], groups=LLAMA3_8B_FUSED) -> list[list[W4A16Linear]]:
+def fuse_layers(layers: list[list[W4A16Linear]], groups=LLAMA3_8B_FUSED,
+                silu_gate: bool = False) -> list[list[W4A16Linear]]:
     """N-concatenate linears that share their input (W4A16Linear.concat: the members' MARLIN
-    words back to back, their scales along N)."""
+    words back to back, their scales along N).  With `silu_gate`, gate|up becomes a
+    W4A16SiluGate (silu(gate) * up, columns interleaved by 8) whose output feeds down."""
     fused = []
     for layer in layers:
         by_name = {lin.name: lin for lin in layer}
         out = []
         for name, members in groups:
-            lin = W4A16Linear.concat([by_name[m] for m in members])
+            parts = [by_name[m] for m in members]
+            if silu_gate and members == ("gate", "up"):
+                lin = W4A16SiluGate.from_members(*parts)
+            else:
+                lin = W4A16Linear.concat(parts)
             if len(members) > 1:
                 lin.name = name
             out.append(lin)
@@ -122,7 +130,14 @@ class W4A16LinearStack:
         self.stream = torch.cuda.Stream(device=self.device)
 
     def forward(self) -> list[torch.Tensor]:
-        return [lin(self.inputs[lin.in_features]) for layer in self.layers for lin in layer]
+        outs = []
+        for layer in self.layers:
+            prev = None
+            for lin in layer:
+                x = outs[-1] if isinstance(prev, W4A16SiluGate) else self.inputs[lin.in_features]
+                outs.append(lin(x))
+                prev = lin
+        return outs
 
     def capture(self) -> None:
         # One eager pass on the capture stream first: it sizes the shared

@@ -100,3 +100,27 @@ def test_fused_stack_equals_unfused(m):
     if m == 1:  # one K slice, 16-column units for every shape: identical plans
         torch.testing.assert_close(yb[0], torch.cat(ya[0:3], dim=1), rtol=0, atol=0)
         torch.testing.assert_close(yb[2], torch.cat(ya[4:6], dim=1), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("m", [1, 32])
+def test_silu_gated_stack(m):
+    """fuse_layers(silu_gate=True): gate|up is one W4A16SiluGate whose output feeds down, as
+    in the model; through the graph its output equals silu(gate) * up of the separate
+    linears (up to their fp16 rounding) and down's output equals down applied eagerly to it."""
+    layers = random_layers(1, device="cuda:0", seed=9)
+    plain = W4A16LinearStack(layers, m, seed=4)
+    gated = W4A16LinearStack(fuse_layers(layers, silu_gate=True), m, seed=4)
+    assert gated.launches_per_step() == 4
+    plain.capture()
+    gated.capture()
+    for _ in range(2):
+        plain.step()
+        gated.step()
+        torch.cuda.synchronize()
+        g, u = plain.outputs[4].float(), plain.outputs[5].float()
+        ref = torch.nn.functional.silu(g) * u
+        h = gated.outputs[2]
+        assert h.shape == (m, 14336)
+        torch.testing.assert_close(h.float(), ref, rtol=4e-3, atol=4e-3 * ref.abs().max().item())
+        down = gated.layers[0][3]
+        torch.testing.assert_close(gated.outputs[3], down(h), rtol=0, atol=0)
