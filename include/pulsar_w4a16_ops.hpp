@@ -57,4 +57,13 @@ at::Tensor gemm_w4a16_gptq_cuda(const at::Tensor& x, const at::Tensor& weight_ma
                                 const std::optional<at::Tensor>& qzeros, const std::optional<at::Tensor>& perm,
                                 int64_t group_size);
 
+// The MLP gate in one op: y [M, N/2] = silu(x @ Wg^T) * (x @ Wu^T) from a
+// gate|up weight interleaved by 8 columns (fused columns 16j..16j+7 gate
+// 8j..8j+7, 16j+8..16j+15 up 8j..8j+7; N % 16 == 0); scales, qzeros and perm as
+// for gemm_w4a16_gptq_cuda in the same column order.  Replaces two at::linear
+// calls and at::silu(gate) * up (pulsar-core/src/model/qwen3.cpp:116-118).
+at::Tensor gemm_w4a16_silu_mul_cuda(const at::Tensor& x, const at::Tensor& weight_marlin, const at::Tensor& scales,
+                                    const std::optional<at::Tensor>& qzeros, const std::optional<at::Tensor>& perm,
+                                    int64_t group_size);
+
 }  // namespace pulsar
