@@ -437,7 +437,7 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.n_end = (int)N;
         a.cus = cu_count();
         a.tile_rows = p.p_tile_rows;
-        e = p.p256 ? launch_prefill256(stype, qzeros != nullptr, a, stream)
+        e = p.p256 ? launch_prefill256(xt, stype, qzeros != nullptr, a, stream)
                    : launch_prefill(layout, xt, stype, qzeros != nullptr, a, stream);
         if (e != hipSuccess) return hip_fail(e);
     }

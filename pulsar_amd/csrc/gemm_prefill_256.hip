@@ -22,10 +22,15 @@
 //
 // Dequant.  Pair p of MARLIN word tg (nibbles p, p+4) holds natural K
 // {8p + 2tg, 8p + 2tg + 1}, so pair p of a column's four words is the K run
-// [8p, 8p + 8) -- exactly what one lane supplies to an MFMA.  Per pair:
-// shift, splice into 1024.0 (exact 1024 + u), subtract 1024 + z (exact), times
-// the group scale (one fp16 rounding, as the reference's dequant_scale,
-// w4a16_marlin.cu:103-113).
+// [8p, 8p + 8) -- exactly what one lane supplies to an MFMA.  fp16 x, per
+// pair: shift, splice into 1024.0 (exact 1024 + u), subtract 1024 + z
+// (exact), times the group scale (one fp16 rounding, as the reference's
+// dequant_scale, w4a16_marlin.cu:103-113).  bf16 x (gfx950 has no packed bf16
+// arithmetic): splice into 128.0 (exact 128 + u), then per value one fp32 fma
+// (128 + u) * s - (128 + z) * s with s the scale rounded to bf16 -- both
+// products are exact in fp32 -- and one v_cvt_pk_bf16_f32 per pair: the
+// reference's bf16 fragment round(q * round(s)) bit for bit
+// (w4a16_marlin.cu:115-126).
 //
 // Reference counterpart: w4a16_marlin_kernel at BM = 64
 // (pulsar-core/src/kernels/w4a16_marlin.cu:197-304).
@@ -86,7 +91,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // the N columns of the last wave; see launch_prefill256).
 // 128-row tiles (RT = 4) use 78 KB of LDS, so two workgroups fit on a CU if
 // each wave keeps to 256 registers (two waves per SIMD).
-template <typename ST, bool ZP, bool PARTIAL, int RT>
+template <bool BF16, typename ST, bool ZP, bool PARTIAL, int RT>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(RT == 4 ? 2 : 1, RT == 4 ? 2 : 1)))
 void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
     constexpr int TMR = 32 * RT;                 // rows of this tile
@@ -167,7 +172,7 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
 
     // splice constant in a VGPR (the mask comes in an SGPR): one v_and_or_b32
     uint32_t one;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(one) : "s"(0x64006400u));
+    asm volatile("v_mov_b32 %0, %1" : "=v"(one) : "s"(BF16 ? 0x43004300u : 0x64006400u));
 
     // One chunk = four 16-K steps; step s is pair s % 2 of 32-K tile s / 2, and
     // this lane's K run in it is [16s + 8hb, +8): activation 16-byte unit
@@ -181,7 +186,8 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) wq[t][ct] = *reinterpret_cast<const u32x4*>(B + t * 1024 + (ct * 32 + c) * 16);
-        f16x2 s2[2], z2[2];
+        f16x2 s2[2], z2[2];   // fp16: scale, 1024 + z
+        float sb[2], cz[2];   // bf16: scale rounded to bf16, -(128 + z) * scale
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
             const int cl = ct * 32 + c;  // column inside the wave's block
@@ -191,11 +197,16 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
             } else {
                 sf = (float)*reinterpret_cast<const _Float16*>(&sS[st][wave * 256 + cl * 2]);
             }
-            const _Float16 sh = (_Float16)sf;
-            s2[ct] = f16x2{sh, sh};
             uint32_t z = 8u;
             if constexpr (ZP) z = (*reinterpret_cast<const uint32_t*>(&sZ[st][wave * 256 + (cl >> 3) * 4]) >> (4 * (cl & 7))) & 0xfu;
-            z2[ct] = as_h2((0x6400u | z) * 0x10001u);  // 1024 + z
+            if constexpr (BF16) {
+                sb[ct] = (float)(__bf16)sf;
+                cz[ct] = -(128.f + (float)z) * sb[ct];
+            } else {
+                const _Float16 sh = (_Float16)sf;
+                s2[ct] = f16x2{sh, sh};
+                z2[ct] = as_h2((0x6400u | z) * 0x10001u);  // 1024 + z
+            }
         }
         auto load_a = [&](int s, u32x4 (&av)[RT]) {
             const int kch = 2 * s + hb;
@@ -212,7 +223,13 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
 #pragma unroll
                 for (int tg = 0; tg < 4; ++tg) {
                     const uint32_t v = ((wq[s >> 1][ct][tg] >> sh) & mk.lo) | one;
-                    bv[ct][tg] = as_u32((as_h2(v) - z2[ct]) * s2[ct]);
+                    if constexpr (BF16) {
+                        bv[ct][tg] = pack_bf16x2_rne(__builtin_fmaf(__builtin_bit_cast(float, v << 16), sb[ct], cz[ct]),
+                                                     __builtin_fmaf(__builtin_bit_cast(float, v & 0xffff0000u), sb[ct],
+                                                                    cz[ct]));
+                    } else {
+                        bv[ct][tg] = as_u32((as_h2(v) - z2[ct]) * s2[ct]);
+                    }
                 }
         };
         u32x4 av[2][RT], bv[2][2];
@@ -228,7 +245,7 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = mfma32x32x16<false>(av[cur][rt], bv[cur][ct], acc[rt][ct]);
+                for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = mfma32x32x16<BF16>(av[cur][rt], bv[cur][ct], acc[rt][ct]);
             // interleave: per A fragment of the next step, two MFMAs and its
             // dequant share
             if (s < 3) {
@@ -237,7 +254,7 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);         // DS read
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 32 / RT, 0);  // VALU
+                    __builtin_amdgcn_sched_group_barrier(0x002, (BF16 ? 56 : 32) / RT, 0);  // VALU
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -284,7 +301,7 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
                         const float g = acc[rt][ct][e];
                         const float u = __shfl_xor(g, 8);
                         const uint32_t off = base + (uint32_t)(r * nh * 2);
-                        __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<false>(silu_mul(g, u)), out, (int)off, 0, 0);
+                        __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<BF16>(silu_mul(g, u)), out, (int)off, 0, 0);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -303,7 +320,7 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
                 for (int e = 0; e < 16; ++e) {
                     const int r = rt * 32 + 8 * (e >> 2) + (e & 3);  // row offset without 4 * hb
                     const uint32_t off = base + (uint32_t)(r * N * 2);
-                    __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<false>(acc[rt][ct][e]), out, (int)off, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<BF16>(acc[rt][ct][e]), out, (int)off, 0, 0);
                 }
             // one fragment at a time keeps the converted values few
                 __builtin_amdgcn_sched_barrier(0);
@@ -338,7 +355,7 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
 bool prefill256_ok(int layout, int xtype, int64_t N, int64_t K, int64_t G) {
     // 32-bit buffer offsets: a 256-row fp32 partial tile of the output must
     // stay below 2 GiB
-    return layout == LAYOUT_MARLIN && xtype == X_F16 && K % TK == 0 && G % TK == 0 && N % 8 == 0 &&
+    return layout == LAYOUT_MARLIN && (xtype == X_F16 || xtype == X_BF16) && K % TK == 0 && G % TK == 0 && N % 8 == 0 &&
            N <= (int64_t{1} << 20);
 }
 
@@ -372,7 +389,7 @@ int64_t prefill256_tail_cols(int64_t M, int64_t N, int cus, double* waves) {
 // done by a second launch with 128-row tiles: twice the workgroups at half the
 // work each, filling the last wave (qkv: 256 full tiles, then 256 half tiles).
 // Same arithmetic per output element, so the result does not change.
-template <typename ST, bool ZP>
+template <bool BF16, typename ST, bool ZP>
 void launch_variant(const PrefillArgs& a, hipStream_t stream) {
     const NibbleMasks mk{};
     const int64_t num_m = ceil_div(a.M, TM), num_n = ceil_div(a.N, TN);
@@ -381,10 +398,10 @@ void launch_variant(const PrefillArgs& a, hipStream_t stream) {
         f.n_begin = 0;
         f.n_end = a.N;
         if (a.tile_rows == TM / 2) {
-            hipLaunchKernelGGL((prefill256_kernel<ST, ZP, true, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * num_n), 1,
+            hipLaunchKernelGGL((prefill256_kernel<BF16, ST, ZP, true, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * num_n), 1,
                                                                           a.splits), dim3(kT), 0, stream, f, mk);
         } else {
-            hipLaunchKernelGGL((prefill256_kernel<ST, ZP, true, 8>), dim3((unsigned)(num_m * num_n), 1, a.splits),
+            hipLaunchKernelGGL((prefill256_kernel<BF16, ST, ZP, true, 8>), dim3((unsigned)(num_m * num_n), 1, a.splits),
                                dim3(kT), 0, stream, f, mk);
         }
         return;
@@ -393,7 +410,7 @@ void launch_variant(const PrefillArgs& a, hipStream_t stream) {
         PrefillArgs h = a;
         h.n_begin = 0;
         h.n_end = a.N;
-        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, false, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * num_n)),
+        hipLaunchKernelGGL((prefill256_kernel<BF16, ST, ZP, false, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * num_n)),
                            dim3(kT), 0, stream, h, mk);
         return;
     }
@@ -403,24 +420,29 @@ void launch_variant(const PrefillArgs& a, hipStream_t stream) {
         PrefillArgs f = a;
         f.n_begin = 0;
         f.n_end = (int)std::min<int64_t>(a.N, nfull * TN);
-        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, false, 8>), dim3((unsigned)(num_m * nfull)), dim3(kT), 0, stream,
+        hipLaunchKernelGGL((prefill256_kernel<BF16, ST, ZP, false, 8>), dim3((unsigned)(num_m * nfull)), dim3(kT), 0, stream,
                            f, mk);
     }
     if (nt > 0) {
         PrefillArgs h = a;
         h.n_begin = (int)(nfull * TN);
         h.n_end = a.N;
-        hipLaunchKernelGGL((prefill256_kernel<ST, ZP, false, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * nt)), dim3(kT),
+        hipLaunchKernelGGL((prefill256_kernel<BF16, ST, ZP, false, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * nt)), dim3(kT),
                            0, stream, h, mk);
     }
 }
 
-hipError_t launch_prefill256(int stype, bool zp, const PrefillArgs& a, hipStream_t stream) {
+template <bool BF16>
+void launch_dtype(int stype, bool zp, const PrefillArgs& a, hipStream_t stream) {
     if (stype == S_F32) {
-        zp ? launch_variant<float, true>(a, stream) : launch_variant<float, false>(a, stream);
+        zp ? launch_variant<BF16, float, true>(a, stream) : launch_variant<BF16, float, false>(a, stream);
     } else {
-        zp ? launch_variant<_Float16, true>(a, stream) : launch_variant<_Float16, false>(a, stream);
+        zp ? launch_variant<BF16, _Float16, true>(a, stream) : launch_variant<BF16, _Float16, false>(a, stream);
     }
+}
+
+hipError_t launch_prefill256(int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream) {
+    xtype == X_BF16 ? launch_dtype<true>(stype, zp, a, stream) : launch_dtype<false>(stype, zp, a, stream);
     return hipGetLastError();
 }
 

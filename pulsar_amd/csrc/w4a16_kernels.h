@@ -113,14 +113,14 @@ hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const Prefi
 int prefill_tile_m();
 int prefill_tile_n();
 
-// Prefill GEMM on a 256 x 256 output tile (MARLIN layout, fp16 activations,
+// Prefill GEMM on a 256 x 256 output tile (MARLIN layout, fp16 or bf16 activations,
 // K and the group size multiples of 64).  Same arguments as launch_prefill.
 bool prefill256_ok(int layout, int xtype, int64_t N, int64_t K, int64_t G);
 int prefill256_tile();
 // Unsplit 256-row launches: N-tile columns run as 128-row tail tiles, and the
 // launch's cost in waves of full tiles (into *waves when not null).
 int64_t prefill256_tail_cols(int64_t M, int64_t N, int cus, double* waves);
-hipError_t launch_prefill256(int stype, bool zp, const PrefillArgs& a, hipStream_t stream);
+hipError_t launch_prefill256(int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream);
 
 // x_out[m, j] = x[m, perm[j]]
 hipError_t launch_gather_x(const uint16_t* x, const int32_t* perm, uint16_t* out, int M, int K, hipStream_t stream);

@@ -119,3 +119,46 @@ def test_prefill_plans_agree_with_oracle(plan_env, rows, splits, m, n):
     check(y32, c.y_ref, torch.float16, f"rows={rows} splits={splits} m={m} n={n} fp32 scales")
     y16 = ops.gemm_w4a16_gptq(c.x, wm, sm.half(), None, None, g)
     check(y16, c.y_ref, torch.float16, f"rows={rows} splits={splits} m={m} n={n} fp16 scales")
+
+
+@pytest.mark.parametrize("m,n,k,g", [(65, 64, 64, 64), (300, 200, 320, 64), (257, 520, 1024, 128),
+                                     (700, 1000, 2048, 64)])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_prefill_bf16(plan_env, m, n, k, g, splits):
+    """bf16 activations on the 256-wide kernel: splice into 128.0, one fp32 fma per value with
+    the bf16-rounded scale, v_cvt_pk_bf16_f32, bf16 MFMA; against the oracle at the bf16
+    tolerance, unsplit and with K slices."""
+    plan_env["PW4_PREFILL_SPLITS"] = str(splits)
+    c = reference_case(m, n, k, g, torch.bfloat16, seed=17)
+    wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float32), g)
+    y = ops.gemm_w4a16_marlin(c.x, wm, sm, g)
+    assert y.dtype == torch.bfloat16
+    check(y, c.y_ref, torch.bfloat16, f"bf16 m={m} n={n} k={k} g={g} splits={splits}")
+
+
+@pytest.mark.parametrize("sym,act", [(True, False), (False, True)])
+def test_prefill_bf16_gptq(sym, act):
+    m, n, k, g = 390, 328, 1024, 64
+    c = baseline_case(m, n, k, g, dtype=torch.bfloat16, seed=18, symmetric=sym, act_order=act)
+    g_idx = torch.from_numpy(c.g_idx).cuda() if act else None
+    wm, perm = ops.repack_w4a16_gptq(c.qweight(), g_idx, g)
+    scales = torch.from_numpy(np.ascontiguousarray(c.scale_nk.T)).half().cuda()
+    y = ops.gemm_w4a16_gptq(c.x, wm, scales, None if sym else c.qzeros(), perm if act else None, g)
+    check(y, c.y_ref, torch.bfloat16, f"bf16 gptq sym={sym} act={act}")
+
+
+def test_prefill_bf16_kernels_agree():
+    """The 256-wide and the 128 x 128 kernels build the same bf16 B fragments and sum in fp32:
+    their outputs agree to bf16 output rounding."""
+    m, n, k, g = 512, 1024, 2048, 128
+    c = reference_case(m, n, k, g, torch.bfloat16, seed=19)
+    wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float32), g)
+    ys = {}
+    for t in (128, 256):
+        os.environ["PW4_PREFILL_TILE"] = str(t)
+        try:
+            ys[t] = ops.gemm_w4a16_marlin(c.x, wm, sm, g).float()
+        finally:
+            del os.environ["PW4_PREFILL_TILE"]
+    diff = (ys[128] - ys[256]).abs().max().item()
+    assert diff <= 1e-2 * ys[128].abs().max().item(), diff
