@@ -152,11 +152,13 @@ struct Plan {
     size_t partial_bytes = 0;
     size_t xperm_bytes = 0;
     size_t silu_tmp_bytes = 0;  // SiLU-gated plans whose kernels cannot pair the columns themselves
+    size_t repack_bytes = 0;    // CT weights repacked per call for the 256-wide kernel (words, then scales)
     // Every non-empty workspace starts with the fixed zero region, so the
     // bytes a decode call uses as counters or exchange slots are never
     // scratch for another call that shares the workspace.
     size_t workspace() const {
-        const size_t rest = align_up(partial_bytes) + align_up(xperm_bytes) + align_up(silu_tmp_bytes);
+        const size_t rest =
+            align_up(partial_bytes) + align_up(xperm_bytes) + align_up(silu_tmp_bytes) + align_up(repack_bytes);
         return (rest || tree) ? kZeroRegion + rest : 0;
     }
 };
@@ -300,9 +302,17 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         // quant group; with its 128-row tiles and K slices it is measured 20-45%
         // faster than the 128 x 128 kernel at M = 72..160 on every Llama-3-8B
         // layer shape, so it takes every M past the decode kernel's.
-        const bool ok256 = prefill256_ok(layout, x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16, N, K, G);
+        const int xt = x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16;
         const int tile_pref = prefill_tile_override();
-        p.p256 = ok256 && tile_pref != 128;
+        p.p256 = prefill256_ok(LAYOUT_MARLIN, xt, N, K, G) && tile_pref != 128;
+        // The CT layout (gemm_w4a16) reaches the 256-wide kernel through a
+        // per-call repack into the workspace: one pass over the weights
+        // (~5 us for 4096 x 4096) against the 128 x 128 kernel's ~2x slower
+        // GEMM at every M past the decode range.
+        if (p.p256 && layout == LAYOUT_CT) {
+            p.repack_bytes = align_up((size_t)round_up(N, kMarlinBN) * round_up(K, kMarlinBK) / 2) +
+                             (size_t)(K / G) * N * sizeof(float);
+        }
         const int64_t tm = p.p256 ? prefill256_tile() : prefill_tile_m();
         const int64_t tn = p.p256 ? prefill256_tile() : prefill_tile_n();
         const int64_t base = ceil_div(M, tm) * ceil_div(N, tn);
@@ -374,8 +384,23 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
     // the GEMM's own output: y, or the workspace copy a second pass gates into y
     uint16_t* y_gemm = silu_tmp ? silu_tmp : reinterpret_cast<uint16_t*>(y);
     const int xt = x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16;
-    const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
     hipError_t e;
+    if (p.repack_bytes) {
+        // CT weights -> MARLIN words and fp32 [K/G, N] scales in the workspace,
+        // then the MARLIN path
+        char* rp = ws + kZeroRegion + align_up(p.partial_bytes) + align_up(p.xperm_bytes) + align_up(p.silu_tmp_bytes);
+        uint32_t* words = reinterpret_cast<uint32_t*>(rp);
+        float* sm = reinterpret_cast<float*>(rp + align_up((size_t)round_up(N, kMarlinBN) * round_up(K, kMarlinBK) / 2));
+        e = launch_repack_ct(w, words, (int)N, (int)K, stream);
+        if (e != hipSuccess) return hip_fail(e);
+        e = launch_scale_transpose(scales, S_F32, sm, (int)N, (int)(K / G), stream);
+        if (e != hipSuccess) return hip_fail(e);
+        layout = LAYOUT_MARLIN;
+        w = words;
+        scales = sm;
+        stype = S_F32;
+    }
+    const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
     const uint16_t* xin = reinterpret_cast<const uint16_t*>(x);
     if (perm) {
         e = launch_gather_x(xin, perm, xperm, (int)M, (int)K, stream);

@@ -1,4 +1,4 @@
-"""GPU parity of the 256 x 256 prefill kernel (MARLIN layout, fp16 activations)
+"""GPU parity of the 256-wide prefill kernel (MARLIN layout, fp16 and bf16 activations)
 against the fp32 oracle, on ragged M / N, every group size it takes, symmetric
 and asymmetric weights with act-order, and forced K splits.  The tile choice is
 pinned through PW4_PREFILL_TILE so that small cases reach this kernel; the

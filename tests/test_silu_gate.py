@@ -10,9 +10,10 @@ The reference runs two at::linear calls and at::silu(gate) * up
 * GPU: gemm_w4a16_silu_mul against silu(g) * u of the fp32 oracle GEMM, on
   every plan that produces it: decode without K slices (the kernel pairs the
   columns), decode with exchange-tree or counter K slices, the 256-wide prefill
-  kernel unsplit and split (split-K combine), and the 128 x 128 kernel (bf16
-  x); the last three kinds gate the GEMM output in a second pass or in the
-  combine.
+  kernel unsplit (fp16 and bf16 x) and split (split-K combine), and the
+  128 x 128 kernel (pinned through PW4_PREFILL_TILE) unsplit and split; the
+  decode K-slice and unsplit 128 x 128 plans gate the GEMM output in a second
+  pass.
 """
 
 import os
@@ -79,7 +80,7 @@ def _silu_ref(y_full: np.ndarray) -> np.ndarray:
 
 @pytest.fixture
 def plan_env():
-    keys = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS")
+    keys = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS", "PW4_PREFILL_TILE")
     old = {k: os.environ.get(k) for k in keys}
     yield os.environ
     for k, v in old.items():
@@ -89,30 +90,31 @@ def plan_env():
             os.environ[k] = v
 
 
-# (m, n = 2F, k, x dtype, prefill splits override, absolute bound).  The absolute bound (max
+# (m, n = 2F, k, x dtype, plan overrides, absolute bound).  The absolute bound (max
 # error within half an fp16 ulp + 1e-2) holds where both GEMM outputs are exact fp32 sums of
 # exact q * s products and the gate is fused: the decode kernel's direct store.  The prefill
 # kernels round q * s to fp16 in the B fragment (as the reference's MMA path does), gated-after
 # plans round gate and up to fp16 first, and the product scales either error by the other
 # factor; those cases are held to the relative bounds (rel-L2 1e-3, max 5e-3 of max |y|).
 CASES = [
-    (1, 512, 512, torch.float16, None, True),      # decode, direct store
-    (16, 1024, 1024, torch.float16, None, True),
-    (5, 4160, 256, torch.float16, None, True),     # N past a 64-column block boundary
-    (24, 512, 4096, torch.float16, None, False),   # decode, exchange-tree K slices
-    (48, 256, 4096, torch.float16, None, False),   # decode, counter K slices (M > 32)
-    (300, 1024, 512, torch.float16, 1, False),     # 256-wide prefill, unsplit
-    (129, 512, 2048, torch.float16, 4, False),     # 256-wide prefill, K slices -> combine
-    (100, 512, 1024, torch.bfloat16, None, False),  # 128 x 128 kernel
+    (1, 512, 512, torch.float16, {}, True),      # decode, direct store
+    (16, 1024, 1024, torch.float16, {}, True),
+    (5, 4160, 256, torch.float16, {}, True),     # N past a 64-column block boundary
+    (24, 512, 4096, torch.float16, {}, False),   # decode, exchange-tree K slices
+    (48, 256, 4096, torch.float16, {}, False),   # decode, counter K slices (M > 32)
+    (300, 1024, 512, torch.float16, {"PW4_PREFILL_SPLITS": "1"}, False),   # 256-wide prefill, unsplit
+    (200, 1024, 512, torch.bfloat16, {"PW4_PREFILL_SPLITS": "1"}, False),  # the same, bf16 x
+    (129, 512, 2048, torch.float16, {"PW4_PREFILL_SPLITS": "4"}, False),   # 256-wide, K slices -> combine
+    (100, 512, 4096, torch.bfloat16, {"PW4_PREFILL_TILE": "128"}, False),  # 128 x 128 kernel, K slices
+    (700, 1024, 256, torch.float16, {"PW4_PREFILL_TILE": "128"}, False),   # 128 x 128 kernel, unsplit
 ]
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m,n,k,dtype,splits,abs_bound", CASES)
+@pytest.mark.parametrize("m,n,k,dtype,env,abs_bound", CASES)
 @pytest.mark.parametrize("sym,act", [(True, False), (False, True)])
-def test_silu_mul_matches_oracle(plan_env, m, n, k, dtype, splits, abs_bound, sym, act):
-    if splits is not None:
-        plan_env["PW4_PREFILL_SPLITS"] = str(splits)
+def test_silu_mul_matches_oracle(plan_env, m, n, k, dtype, env, abs_bound, sym, act):
+    plan_env.update(env)
     c = baseline_case(m, n, k, G, dtype=dtype, seed=m + n, symmetric=sym, act_order=act)
     g_idx = torch.from_numpy(c.g_idx).cuda() if act else None
     wm, perm = ops.repack_w4a16_gptq(c.qweight(), g_idx, G)
