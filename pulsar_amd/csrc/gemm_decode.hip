@@ -40,6 +40,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 
 #include "w4a16_common.h"
 #include "w4a16_kernels.h"
@@ -298,19 +299,53 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     }
     __syncthreads();
     if constexpr (BF16) {
-        // per-step corrections, stored negated: -(128 P + z Q) with P = Q = sum(x)
-        for (int i = tid; i < M * nsteps * NGRP; i += kThreads) {
-            const int m = i % M, sg = i / M, st = sg / NGRP, gi = sg - st * NGRP;
-            const int k0 = st * 128 + gi * (128 / NGRP), k1 = k0 + 128 / NGRP;
-            float p = 0.f;
-            for (int k = k0; k < k1; ++k) p += half_to_f32<true>(smem[m * rs + k]);
-            const int idx = (st * NGRP + gi) * MP + m;
-            if constexpr (ZP) {
-                CP[idx] = -128.f * p;
-                CQ[idx] = -p;
-            } else {
-                CP[idx] = -136.f * p;
+        // per-step corrections, stored negated: -(128 P + z Q) with P = Q = sum(x).
+        // Each sum is (128 / NGRP) / 8 16-byte chunks.  With few sums (small M)
+        // a sum spreads over an aligned group of L lanes, the most that keep the
+        // pass to one round over the workgroup, and ends in a butterfly; with
+        // many, each thread reads its sum's chunks itself.  L is a compile-time
+        // choice so that every variant's loops unroll.
+        constexpr int kChunks = 16 / NGRP;
+        const int items = M * nsteps * NGRP;
+        auto corr_pass = [&](auto lanes) {
+            constexpr int L = decltype(lanes)::value, cpl = kChunks / L;
+            const int part = tid & (L - 1);
+            for (int base = 0; base < items; base += kThreads / L) {
+                const int i = base + tid / L;  // the same for the whole group
+                if (i < items) {
+                    const int m = i % M, sg = i / M, st = sg / NGRP, gi = sg - st * NGRP;
+                    const int k = st * 128 + gi * (128 / NGRP) + part * cpl * 8;
+                    float p = 0.f;
+#pragma unroll
+                    for (int ch = 0; ch < cpl; ++ch) {
+                        const u32x4 v = *reinterpret_cast<const u32x4*>(smem + m * rs + k + ch * 8);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            p += __builtin_bit_cast(float, v[e] << 16) + __builtin_bit_cast(float, v[e] & 0xffff0000u);
+                        }
+                    }
+#pragma unroll
+                    for (int off = L / 2; off > 0; off >>= 1) p += __shfl_xor(p, off);
+                    if (part == 0) {
+                        const int idx = (st * NGRP + gi) * MP + m;
+                        if constexpr (ZP) {
+                            CP[idx] = -128.f * p;
+                            CQ[idx] = -p;
+                        } else {
+                            CP[idx] = -136.f * p;
+                        }
+                    }
+                }
             }
+        };
+        if (items * kChunks <= kThreads) {
+            corr_pass(std::integral_constant<int, kChunks>{});
+        } else if (items * 4 <= kThreads) {
+            corr_pass(std::integral_constant<int, 4>{});
+        } else if (items * 2 <= kThreads) {
+            corr_pass(std::integral_constant<int, 2>{});
+        } else {
+            corr_pass(std::integral_constant<int, 1>{});
         }
         __syncthreads();
     }
