@@ -111,6 +111,27 @@ def cpu_baseline(time_budget_s: float = 12.0) -> dict:
                 tot_time += time.perf_counter() - t0
                 tot_bytes += decode_bytes(m, k, n)
                 gemms += 1
+    # BASELINE configs[0] (M = 1, K = N = 4096) on the same path, its two phases timed apart:
+    # median of 5 runs each
+    k1 = n1 = 4096
+    packed1 = rng.integers(-(2 ** 31), 2 ** 31, size=(n1, k1 // 8), dtype=np.int64).astype(np.int32)
+    scale1 = (np.abs(rng.standard_normal((n1, k1 // G))) * 0.02 + 1e-3).astype(np.float32)
+    x1 = rng.standard_normal((1, k1)).astype(np.float32)
+    phases = {"dequant": [], "gemm": [], "total": []}
+    w1 = np.empty((n1, k1), dtype=np.float32)
+    for _ in range(6):  # the first pass faults the buffer in; medians over the last 5
+        t0 = time.perf_counter()
+        O.dequant_ct(packed1, scale1, G, out=w1)
+        t1 = time.perf_counter()
+        O.gemm_f32(x1, w1)
+        t2 = time.perf_counter()
+        O.w4a16_ct_forward(x1, packed1, scale1, G, w1)
+        t3 = time.perf_counter()
+        phases["dequant"].append(t1 - t0)
+        phases["gemm"].append(t2 - t1)
+        phases["total"].append(t3 - t2)
+    config1 = {f"{k}_ms": round(sorted(v[1:])[2] * 1e3, 3) for k, v in phases.items()}
+    config1["GB/s"] = round(decode_bytes(1, k1, n1) / (sorted(phases["total"][1:])[2]) / 1e9, 3)
     return {
         "value": round(tot_bytes / tot_time / 1e9, 3),
         "unit": "GB/s",
@@ -118,6 +139,7 @@ def cpu_baseline(time_budget_s: float = 12.0) -> dict:
         "kind": "port",
         "sample": f"{gemms // 16} passes over the 16 decode-sweep GEMMs ({gemms} GEMMs, {tot_time:.1f} s of CPU "
                   "work): dequantize to fp32 + OpenMP fp32 GEMM, oracle/w4a16_oracle.c",
+        "config1_m1_k4096_n4096": config1,
     }
 
 
@@ -457,6 +479,23 @@ def main() -> int:
                    "per_gemm_us": {f"{name}_m{m}": round(ms * 1e3, 2) for (m, name, _, _), ms in zip(shapes, per2)}}
         del g2
 
+    # achievable-HBM context: a 512 MiB device-to-device copy (read + write bytes)
+    copy_ceiling = None
+    if not args.no_decode:
+        src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
+        for a, b in ev:
+            a.record()
+            dst.copy_(src)
+            b.record()
+        torch.cuda.synchronize()
+        ms = sorted(a.elapsed_time(b) for a, b in ev)[2]
+        copy_ceiling = {"GB/s": round(2 * COPY_BYTES / (ms * 1e-3) / 1e9, 1), "bytes_moved": 2 * COPY_BYTES,
+                        "what": "torch copy_ of 512 MiB fp16 on the device, median of 5, read + write bytes"}
+        del src, dst
+
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "decode_traffic.json")
     if os.path.exists(tpath):
@@ -531,6 +570,7 @@ def main() -> int:
             "frac": None if achieved is None else round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "mean_launch_us": None if mean_launch_us is None else round(mean_launch_us, 3),
+            "copy_ceiling": copy_ceiling,
         },
         "decode": per_gemm,
         "reference_api": ref_api,

@@ -267,11 +267,13 @@ def repack_gptq_marlin(qweight: np.ndarray, perm_: np.ndarray | None = None) -> 
 # ---- dequant / GEMM ------------------------------------------------------------
 
 
-def dequant_ct(packed: np.ndarray, scale: np.ndarray, group_size: int) -> np.ndarray:
+def dequant_ct(packed: np.ndarray, scale: np.ndarray, group_size: int, out: np.ndarray | None = None) -> np.ndarray:
     packed = np.ascontiguousarray(packed, dtype=np.int32)
     scale = np.ascontiguousarray(scale, dtype=np.float32)
     n, w = packed.shape
-    out = np.empty((n, w * 8), dtype=np.float32)
+    if out is None:
+        out = np.empty((n, w * 8), dtype=np.float32)
+    assert out.shape == (n, w * 8) and out.dtype == np.float32 and out.flags.c_contiguous
     _check(lib().orc_dequant_ct(_p(packed), _p(scale), n, w * 8, group_size, _p(out)), "dequant_ct")
     return out
 
