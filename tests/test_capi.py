@@ -37,6 +37,11 @@ def lib():
     L.pw4_gemm_w4a16_workspace_size.argtypes = [I64, I64, I64, I64, I64]
     L.pw4_gemm_w4a16_marlin_workspace_size.restype = ctypes.c_size_t
     L.pw4_gemm_w4a16_marlin_workspace_size.argtypes = [I64, I64, I64, I64, ctypes.c_int, I64]
+    L.pw4_gemm_w4a16_silu_mul.restype = ctypes.c_int
+    L.pw4_gemm_w4a16_silu_mul.argtypes = [P, ctypes.c_int, P, P, ctypes.c_int, P, P, P, I64, I64, I64, I64, P,
+                                          ctypes.c_size_t, P]
+    L.pw4_gemm_w4a16_silu_mul_workspace_size.restype = ctypes.c_size_t
+    L.pw4_gemm_w4a16_silu_mul_workspace_size.argtypes = [I64, I64, I64, I64, ctypes.c_int]
     L.pw4_repack_w4a16.restype = ctypes.c_int
     L.pw4_repack_w4a16.argtypes = [P, P, ctypes.c_int, I64, I64, I64, P, P, P]
     L.pw4_gidx_to_perm.restype = ctypes.c_int
@@ -89,6 +94,13 @@ def test_argument_checks_fire_before_launch(lib):
     assert lib.pw4_gemm_w4a16(odd, 0, dummy, dummy, dummy, 4, 64, 128, 64, 0, None, 0, None) == -1
     assert lib.pw4_gemm_w4a16_marlin(dummy, 0, odd, dummy, 2, None, None, dummy, 4, 64, 128, 64, 0, None, 0,
                                      None) == -1
+    # SiLU-gated GEMM: N (gate|up interleaved by 8) must be a multiple of 16; scale dtype
+    assert lib.pw4_gemm_w4a16_silu_mul(dummy, 0, dummy, dummy, 0, None, None, dummy, 4, 24, 128, 64, None, 0,
+                                       None) == -2
+    assert lib.pw4_gemm_w4a16_silu_mul(dummy, 0, dummy, dummy, 7, None, None, dummy, 4, 32, 128, 64, None, 0,
+                                       None) == -1
+    assert lib.pw4_gemm_w4a16_silu_mul(None, 0, None, None, 0, None, None, None, 0, 32, 128, 64, None, 0, None) == 0
+    assert lib.pw4_gemm_w4a16_silu_mul_workspace_size(4, 24, 128, 64, 0) == 0
     # M == 0 and N == 0 are no-ops (w4a16_gemm.cu:355-357)
     assert lib.pw4_gemm_w4a16(None, 0, None, None, None, 0, 64, 128, 64, 0, None, 0, None) == 0
     assert lib.pw4_gemm_w4a16(None, 0, None, None, None, 4, 0, 128, 64, 0, None, 0, None) == 0
