@@ -143,6 +143,24 @@ def cpu_baseline(time_budget_s: float = 12.0) -> dict:
     }
 
 
+def device_info(torch, dev) -> dict:
+    """Name, compute units and, where rocm-smi answers, the current clocks (taken right after
+    the timed decode sweep, so under load or just after it)."""
+    import subprocess
+
+    props = torch.cuda.get_device_properties(dev)
+    info = {"name": torch.cuda.get_device_name(dev), "arch": getattr(props, "gcnArchName", None),
+            "compute_units": props.multi_processor_count, "clocks": None}
+    try:
+        r = subprocess.run(["rocm-smi", "--showclocks", "--json"], capture_output=True, text=True, timeout=10)
+        if r.returncode == 0:
+            card = next(iter(json.loads(r.stdout).values()))
+            info["clocks"] = {k: v for k, v in card.items() if "clock" in k.lower() and ("sclk" in k or "mclk" in k)}
+    except (OSError, ValueError, StopIteration, AttributeError, subprocess.SubprocessError):
+        pass
+    return info
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -471,6 +489,8 @@ def main() -> int:
         achieved = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) / (sum(each_ms) * 1e-3) / 1e9
         mean_launch_us = sum(each_ms) / len(each_ms) * 1e3
 
+    device = device_info(torch, dev)
+
     ref_api = None
     if not args.no_reference_api:
         g2 = build_graphs(torch, shapes, weights, xs, gemm_reference_api, stream)
@@ -552,6 +572,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic",
+        "device": device,
         "config": {
             "workload": "llama3-8b W4A16 decode sweep: M in {1,4,8,16} x {qkv 4096x6144, o 4096x4096, "
                         "gate_up 4096x28672, down 14336x4096}, symmetric int4 G=128 fp16 scales, MARLIN "
