@@ -389,23 +389,42 @@ def act_order_bench(torch, dev, steps: int, warmup: int) -> dict:
     return out
 
 
-def time_each_launch(torch, shapes, weights, xs, fn, stream, reps: int) -> list[float]:
-    """Mean duration (ms) of single launches, each bracketed by HIP events on
-    the launch stream: the kernel's own time without the back-to-back launch
-    gap, comparable with rocprofv3's per-dispatch durations."""
-    out = []
+def time_each_launch(torch, shapes, weights, xs, fn, stream, reps: int) -> tuple[list[float], list[float]]:
+    """Per shape, the mean duration (ms) of single decode-kernel launches, two ways:
+    * the kernel's own: each call arms pw4_time_next_kernel with a pair of HIP events,
+      which the library passes to hipExtLaunchKernel; they take the dispatch's start and
+      end timestamps, the interval rocprofv3's kernel trace reports;
+    * the call's: HIP events recorded on the launch stream around unarmed calls, which
+      also hold the queue latency in front of the kernel (about 2 us).
+    Under rocprofv3 the armed events read several microseconds longer than the trace's
+    durations of the same dispatches; run without the profiler for these figures."""
+    from pulsar_amd import capi
+
+    lib = capi()
+    own, call = [], []
     with torch.cuda.stream(stream):
         for mi, (m, name, k, n) in enumerate(shapes):
             first = (DECODE_M.index(m) % 2) * REPS
-            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-            for r, (a, b) in enumerate(ev):
-                w = weights[name][(first + r) % COPIES]
+            kev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            cev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for a, b in kev:  # create the events before handing them over
                 a.record(stream)
-                fn(xs[(m, k)], w)
                 b.record(stream)
+            for r in range(reps):  # unarmed calls: a hooked launch costs the runtime more
+                cev[r][0].record(stream)
+                fn(xs[(m, k)], weights[name][(first + r) % COPIES])
+                cev[r][1].record(stream)
+            for r in range(reps):
+                if lib.pw4_time_next_kernel(kev[r][0], kev[r][1]) != 0:
+                    raise RuntimeError("pw4_time_next_kernel failed")
+                fn(xs[(m, k)], weights[name][(first + r) % COPIES])
             stream.synchronize()
-            out.append(sum(a.elapsed_time(b) for a, b in ev) / reps)
-    return out
+            ko = [a.elapsed_time(b) for a, b in kev]
+            if min(ko) <= 0.0:
+                raise RuntimeError(f"kernel timing events did not fire for {name} M={m}")
+            own.append(sum(ko) / reps)
+            call.append(sum(a.elapsed_time(b) for a, b in cev) / reps)
+    return own, call
 
 
 def main() -> int:
@@ -468,7 +487,7 @@ def main() -> int:
         torch.cuda.synchronize()
         return 0
 
-    value = achieved = wall = mean_launch_us = None
+    value = achieved = wall = mean_launch_us = mean_call_us = None
     per_gemm = {}
     launches = args.steps * REPS
     tot_bytes = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) * launches
@@ -483,11 +502,14 @@ def main() -> int:
         value = tot_bytes / wall / 1e9
         del graphs
         # the roofline: algorithmic bytes over the kernel's own duration
-        each_ms = time_each_launch(torch, shapes, weights, xs, gemm_fp16_scales, stream, args.steps * REPS)
-        for (m, name, k, n), ms in zip(shapes, each_ms):
+        each_ms, call_ms = time_each_launch(torch, shapes, weights, xs, gemm_fp16_scales, stream,
+                                            args.steps * REPS)
+        for (m, name, k, n), ms, cms in zip(shapes, each_ms, call_ms):
             per_gemm[f"{name}_m{m}"]["kernel_us"] = round(ms * 1e3, 2)
+            per_gemm[f"{name}_m{m}"]["call_us"] = round(cms * 1e3, 2)
         achieved = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) / (sum(each_ms) * 1e-3) / 1e9
         mean_launch_us = sum(each_ms) / len(each_ms) * 1e3
+        mean_call_us = sum(call_ms) / len(call_ms) * 1e3
 
     device = device_info(torch, dev)
 
@@ -591,6 +613,11 @@ def main() -> int:
             "frac": None if achieved is None else round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "mean_launch_us": None if mean_launch_us is None else round(mean_launch_us, 3),
+            "timing": "achieved = mean algorithmic bytes / mean decode-kernel duration over single launches of "
+                      "the 16 shapes; each duration from a HIP event pair that hipExtLaunchKernel fills with "
+                      "the dispatch's own start and end (pw4_time_next_kernel), the interval rocprofv3's "
+                      "kernel trace reports",
+            "mean_call_us": None if mean_call_us is None else round(mean_call_us, 3),
             "copy_ceiling": copy_ceiling,
         },
         "decode": per_gemm,

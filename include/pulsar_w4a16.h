@@ -59,6 +59,17 @@ typedef struct ihipStream_t* pw4_stream_t; /* == hipStream_t */
 const char* pw4_status_string(int status);
 /* Text of the last HIP error seen by this thread inside the library. */
 const char* pw4_last_hip_error(void);
+/* Kernel timing (no counterpart in the reference; for benchmarks).  Arms the
+ * calling thread: the next GEMM call on this thread that launches the decode
+ * kernel launches it through hipExtLaunchKernel with these two events
+ * (hipEvent_t, created with timing enabled on the GEMM's device), which then
+ * hold that dispatch's own start and end timestamps: the interval a kernel
+ * trace reports, without the queue latency in front of the kernel.  Read them
+ * with hipEventElapsedTime after the stream syncs.  One launch per arming;
+ * (NULL, NULL) disarms; exactly one NULL is PW4_ERR_ARG.  Not for use under
+ * graph capture. */
+int pw4_time_next_kernel(void* start_event, void* stop_event);
+
 /* ABI version of this header: bumped on any incompatible change. */
 int pw4_abi_version(void);
 #define PW4_ABI_VERSION 2

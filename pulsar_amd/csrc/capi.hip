@@ -13,6 +13,18 @@
 
 using namespace pw4;
 
+namespace pw4 {
+// pw4_time_next_kernel's events, armed for the calling thread's next decode
+// kernel launch
+thread_local hipEvent_t g_timing_start = nullptr, g_timing_stop = nullptr;
+
+void take_timing_events(hipEvent_t* start, hipEvent_t* stop) {
+    *start = g_timing_start;
+    *stop = g_timing_stop;
+    g_timing_start = g_timing_stop = nullptr;
+}
+}  // namespace pw4
+
 namespace {
 
 thread_local char g_last_hip_error[256] = "";
@@ -495,6 +507,13 @@ const char* pw4_status_string(int status) {
 }
 
 const char* pw4_last_hip_error(void) { return g_last_hip_error; }
+
+int pw4_time_next_kernel(void* start_event, void* stop_event) {
+    if ((start_event == nullptr) != (stop_event == nullptr)) return PW4_ERR_ARG;
+    pw4::g_timing_start = static_cast<hipEvent_t>(start_event);
+    pw4::g_timing_stop = static_cast<hipEvent_t>(stop_event);
+    return PW4_OK;
+}
 
 int pw4_abi_version(void) { return PW4_ABI_VERSION; }
 

@@ -42,6 +42,8 @@
 #include <tuple>
 #include <type_traits>
 
+#include <hip/hip_ext.h>
+
 #include "w4a16_common.h"
 #include "w4a16_kernels.h"
 
@@ -792,6 +794,14 @@ hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const Decode
     if (x_slots(a.M, a.k_per_split) * spr >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
     hipError_t e = prepare(fn, cfg.lds_bytes);
     if (e != hipSuccess) return e;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    take_timing_events(&t0, &t1);
+    if (t0 != nullptr) {
+        // the events take this dispatch's own start and end timestamps
+        void* args[] = {const_cast<DecodeArgs*>(&a)};
+        return hipExtLaunchKernel(reinterpret_cast<const void*>(fn), dim3(a.wps, a.splits), dim3(kThreads), args,
+                                  cfg.lds_bytes, stream, t0, t1, 0);
+    }
     hipLaunchKernelGGL(fn, dim3(a.wps, a.splits), dim3(kThreads), cfg.lds_bytes, stream, a);
     return hipGetLastError();
 }

@@ -79,6 +79,10 @@ int decode_threads();
 int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree,
                          size_t lds);
 
+// Events armed on the calling thread by pw4_time_next_kernel for its next
+// decode-kernel launch; returns them (nulls when none) and disarms.
+void take_timing_events(hipEvent_t* start, hipEvent_t* stop);
+
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          hipStream_t stream);
 hipError_t launch_combine(const float* partial, uint16_t* y, int64_t mn, int splits, int xtype, hipStream_t stream);

@@ -49,6 +49,8 @@ def lib():
     L.pw4_repack_gptq.restype = ctypes.c_int
     L.pw4_repack_gptq.argtypes = [P, P, I64, I64, P, P]
     L.pw4_abi_version.restype = ctypes.c_int
+    L.pw4_time_next_kernel.restype = ctypes.c_int
+    L.pw4_time_next_kernel.argtypes = [P, P]
     return L
 
 
@@ -70,6 +72,13 @@ def test_status_strings_and_version(lib):
     for code in (-1, -2, -3, -4, -5):
         assert lib.pw4_status_string(code) != b"unknown status"
     assert lib.pw4_abi_version() == 2
+
+
+def test_timing_hook_arguments(lib):
+    # one event without the other is rejected and arms nothing; (NULL, NULL) disarms
+    assert lib.pw4_time_next_kernel(None, P(0x1000)) == -1
+    assert lib.pw4_time_next_kernel(P(0x1000), None) == -1
+    assert lib.pw4_time_next_kernel(None, None) == 0
 
 
 def test_marlin_words_matches_oracle(lib, orc):
