@@ -226,8 +226,13 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         // that allows while every CU still gets three unit slices to balance
         // over at 64 columns, two at 32: a wider unit gives each K wave more
         // steps between unit ends (measured: gate_up at M = 32 30 us with
-        // 32-column units against 37 with 16, down at M = 16 13.8 against 15.1;
-        // qkv and o, one slice per CU at 32 columns, are faster at 16).
+        // 32-column units against 37 with 16, down at M = 16 13.8 against 15.1).
+        // Where the slice's LDS leaves room for one workgroup per CU, 32
+        // columns also win at one slice per CU when the busiest CU gets no more
+        // columns than at 16 (down at M = 8 11.6 us against 12.5, o at M = 24
+        // 8.7 against 9.2); qkv at M = 24-32 (1.5 slices per CU at 32) stays at
+        // 16, and so do slices small enough for two workgroups per CU (down at
+        // M = 5: 11.1 us at 16 against 14.3).
         bool tree = false;
         int tree_nb = 16;
         if (!forced) {
@@ -236,10 +241,14 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
                 int64_t p2 = 2;
                 while (p2 < s2) p2 *= 2;
                 const int nb_forced = decode_nb_override();
+                const bool one_wg_per_cu = 2 * lds_for(p2) > kLdsPerCu;
+                const int64_t busiest16 = ceil_div(ceil_div(ncols, 16) * p2, (int64_t)cus) * 16;
                 for (int w : {64, 32, 16}) {
                     const bool fits = M * w <= 1024 && ncols % w == 0;
-                    if (nb_forced ? (w == nb_forced && fits) || w == 16
-                                  : fits && (ceil_div(ncols, w) * p2 >= (w == 64 ? 3 : 2) * cus || w == 16)) {
+                    const int64_t q = ceil_div(ncols, w) * p2;  // unit slices
+                    const bool wide = q >= (w == 64 ? 3 : 2) * cus ||
+                                      (w == 32 && one_wg_per_cu && ceil_div(q, (int64_t)cus) * 32 <= busiest16);
+                    if (nb_forced ? (w == nb_forced && fits) || w == 16 : (fits && wide) || w == 16) {
                         tree_nb = w;
                         break;
                     }
