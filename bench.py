@@ -420,10 +420,9 @@ def time_each_launch(torch, shapes, weights, xs, fn, stream, reps: int) -> tuple
                 fn(xs[(m, k)], weights[name][(first + r) % COPIES])
             stream.synchronize()
             ko = [a.elapsed_time(b) for a, b in kev]
-            if min(ko) <= 0.0:
-                raise RuntimeError(f"kernel timing events did not fire for {name} M={m}")
-            own.append(sum(ko) / reps)
             call.append(sum(a.elapsed_time(b) for a, b in cev) / reps)
+            # events the runtime left unset read <= 0: then the call's figure stands in
+            own.append(sum(ko) / reps if min(ko) > 0.0 else None)
     return own, call
 
 
@@ -488,6 +487,7 @@ def main() -> int:
         return 0
 
     value = achieved = wall = mean_launch_us = mean_call_us = None
+    hook_ok = False
     per_gemm = {}
     launches = args.steps * REPS
     tot_bytes = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) * launches
@@ -504,6 +504,8 @@ def main() -> int:
         # the roofline: algorithmic bytes over the kernel's own duration
         each_ms, call_ms = time_each_launch(torch, shapes, weights, xs, gemm_fp16_scales, stream,
                                             args.steps * REPS)
+        hook_ok = all(ms is not None for ms in each_ms)
+        each_ms = [c if ms is None else ms for ms, c in zip(each_ms, call_ms)]
         for (m, name, k, n), ms, cms in zip(shapes, each_ms, call_ms):
             per_gemm[f"{name}_m{m}"]["kernel_us"] = round(ms * 1e3, 2)
             per_gemm[f"{name}_m{m}"]["call_us"] = round(cms * 1e3, 2)
@@ -613,10 +615,13 @@ def main() -> int:
             "frac": None if achieved is None else round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "mean_launch_us": None if mean_launch_us is None else round(mean_launch_us, 3),
-            "timing": "achieved = mean algorithmic bytes / mean decode-kernel duration over single launches of "
-                      "the 16 shapes; each duration from a HIP event pair that hipExtLaunchKernel fills with "
-                      "the dispatch's own start and end (pw4_time_next_kernel), the interval rocprofv3's "
-                      "kernel trace reports",
+            "timing": None if achieved is None else (
+                "achieved = mean algorithmic bytes / mean decode-kernel duration over single launches of "
+                "the 16 shapes; each duration from a HIP event pair that hipExtLaunchKernel fills with "
+                "the dispatch's own start and end (pw4_time_next_kernel), the interval rocprofv3's "
+                "kernel trace reports" if hook_ok else
+                "achieved = mean algorithmic bytes / mean duration of HIP events around single calls "
+                "(the kernel timing events did not fire on this box; queue latency included)"),
             "mean_call_us": None if mean_call_us is None else round(mean_call_us, 3),
             "copy_ceiling": copy_ceiling,
         },
