@@ -17,8 +17,11 @@
 // every outstanding LDS copy before each LDS read.  The kernel counts them
 // itself instead: every wave issues the same number of copies per chunk, so
 // "chunk i has landed" is vmcnt <= (copies of chunk i+1), then a barrier.
-// Activation rows are XOR-swizzled in 16-byte units (chunk ^ (row & 7)) so
-// the 32 rows an MFMA reads hit distinct LDS banks.
+// Activation rows are XOR-swizzled in 16-byte units (chunk ^ ((row >> 1) & 7)):
+// rows r and r + 8 of one ds_read_b128 land on different banks.  gfx950 counts
+// no LDS bank conflicts with this swizzle; with chunk ^ (row & 7) it counted
+// 43% of LDS-active cycles as conflict stalls (SQ_LDS_BANK_CONFLICT, gate_up
+// at M = 4096).
 //
 // Dequant.  Pair p of MARLIN word tg (nibbles p, p+4) holds natural K
 // {8p + 2tg, 8p + 2tg + 1}, so pair p of a column's four words is the K run
@@ -141,7 +144,7 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
 #pragma unroll
         for (int i = 0; i < RT; ++i) {
             const int row = wave * (8 * RT) + i * 8 + (lane >> 3);
-            const int kch = (lane & 7) ^ (row & 7);
+            const int kch = (lane & 7) ^ ((row >> 1) & 7);
             const int gm = min(m0 + row, M - 1);
             lds_copy16(a.x + (int64_t)gm * K + kc * TK + kch * 8, abase + i * 64 * 16);
         }
@@ -213,7 +216,7 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
                 const int row = rt * 32 + c;
-                av[rt] = *reinterpret_cast<const u32x4*>(A + row * (TK * 2) + ((kch ^ (row & 7)) * 16));
+                av[rt] = *reinterpret_cast<const u32x4*>(A + row * (TK * 2) + ((kch ^ ((row >> 1) & 7)) * 16));
             }
         };
         auto dequant = [&](int s, u32x4 (&bv)[2]) {
