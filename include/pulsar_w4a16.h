@@ -59,15 +59,18 @@ typedef struct ihipStream_t* pw4_stream_t; /* == hipStream_t */
 const char* pw4_status_string(int status);
 /* Text of the last HIP error seen by this thread inside the library. */
 const char* pw4_last_hip_error(void);
-/* Kernel timing (no counterpart in the reference; for benchmarks).  Arms the
- * calling thread: the next GEMM call on this thread that launches the decode
- * kernel launches it through hipExtLaunchKernel with these two events
- * (hipEvent_t, created with timing enabled on the GEMM's device), which then
- * hold that dispatch's own start and end timestamps: the interval a kernel
- * trace reports, without the queue latency in front of the kernel.  Read them
- * with hipEventElapsedTime after the stream syncs.  One launch per arming;
- * (NULL, NULL) disarms; exactly one NULL is PW4_ERR_ARG.  Not for use under
- * graph capture. */
+/* Kernel timing (no counterpart in the reference; a profiling facility).
+ * Arms the calling thread for its next GEMM call (pw4_gemm_w4a16,
+ * pw4_gemm_w4a16_marlin or pw4_gemm_w4a16_silu_mul): that call takes the two
+ * events (hipEvent_t, created with timing enabled on the GEMM's device) before
+ * it checks its arguments, so they never outlive it, and launches its GEMM
+ * kernels through hipExtLaunchKernel with them: `start` takes the start of
+ * the first GEMM dispatch, `stop` the end of the last -- the interval a
+ * kernel trace reports, without the queue latency in front of the kernel.  A
+ * repack, gather, split-K combine or SiLU pass of the call is not inside it;
+ * a call that fails or launches nothing leaves the events unset.  Read them
+ * with hipEventElapsedTime after the stream syncs.  (NULL, NULL) disarms;
+ * exactly one NULL is PW4_ERR_ARG.  Not for use under graph capture. */
 int pw4_time_next_kernel(void* start_event, void* stop_event);
 
 /* ABI version of this header: bumped on any incompatible change. */

@@ -14,14 +14,13 @@
 using namespace pw4;
 
 namespace pw4 {
-// pw4_time_next_kernel's events, armed for the calling thread's next decode
-// kernel launch
-thread_local hipEvent_t g_timing_start = nullptr, g_timing_stop = nullptr;
+// pw4_time_next_kernel's events, armed for the calling thread's next GEMM call
+thread_local KernelEvents g_armed_events;
 
-void take_timing_events(hipEvent_t* start, hipEvent_t* stop) {
-    *start = g_timing_start;
-    *stop = g_timing_stop;
-    g_timing_start = g_timing_stop = nullptr;
+KernelEvents take_kernel_events() {
+    const KernelEvents ev = g_armed_events;
+    g_armed_events = KernelEvents{};
+    return ev;
 }
 }  // namespace pw4
 
@@ -119,13 +118,22 @@ struct Prefill256Plan {
     int64_t splits;
 };
 
-Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus) {
+// Exact scaling of the 256-wide prefill kernel with fp16 activations (see
+// gemm_prefill_256.hip): on unless PW4_PREFILL_EXACT=0 (A/B sweeps only).
+bool prefill_exact_enabled() {
+    const char* e = std::getenv("PW4_PREFILL_EXACT");
+    return !(e && e[0] == '0');
+}
+
+// only128: 128-row tiles only (the exact-scaling kernel has no 256-row variant)
+Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, bool only128) {
     constexpr double kChunkUs = 2.0, kHalfChunk = 0.6, kShare = 0.8, kPartialBps = 6.0e12, kCombineUs = 2.0;
     Prefill256Plan best{256, 1};
     double best_us = 0.0;
     bool have = false;
     const int64_t num_n = ceil_div(N, 256);
     for (int rows : {256, 128}) {
+        if (only128 && rows != 128) continue;
         for (int64_t s : {1, 2, 3, 4, 6, 8}) {
             if (s > nchunks) break;
             const int64_t cps = ceil_div(nchunks, s);
@@ -155,6 +163,7 @@ struct Plan {
     bool decode = false;
     bool tree = false;       // decode K slices reduced through the exchange tree
     bool p256 = false;       // prefill on the 256 x 256 tile kernel
+    bool p_exact = false;    // ... with exact scaling (fp16 x, 128-row tiles)
     DecodeConfig dc{};
     int p_splits = 1;        // prefill K splits
     int p_cps = 0;           // prefill chunks per split
@@ -326,6 +335,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         const int xt = x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16;
         const int tile_pref = prefill_tile_override();
         p.p256 = prefill256_ok(LAYOUT_MARLIN, xt, N, K, G) && tile_pref != 128;
+        p.p_exact = p.p256 && xt == X_F16 && prefill_exact_enabled();
         // The CT layout (gemm_w4a16) reaches the 256-wide kernel through a
         // per-call repack into the workspace: one pass over the weights
         // (~5 us for 4096 x 4096) against the 128 x 128 kernel's ~2x slower
@@ -345,7 +355,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         } else if (p.p256 && prefill_splits_override()) {
             s = std::min<int64_t>(prefill_splits_override(), std::max<int64_t>(nchunks, 1));
         } else if (p.p256) {
-            const Prefill256Plan pp = plan_prefill256(M, N, nchunks, cus);
+            const Prefill256Plan pp = plan_prefill256(M, N, nchunks, cus, p.p_exact);
             s = pp.splits;
             p.p_tile_rows = pp.rows;
         } else if (base >= cus || nchunks < 8) {
@@ -362,6 +372,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         p.use_partial = forced || s > 1;
         if (p.use_partial) p.partial_bytes = (size_t)p.splits * M * N * 4;
         if (p.p256 && prefill_rows_override()) p.p_tile_rows = prefill_rows_override();
+        if (p.p_exact) p.p_tile_rows = 128;
     }
     // act-order: x is gathered once per call into the workspace, for either
     // kernel (each decode workgroup would otherwise gather the same slice)
@@ -385,9 +396,12 @@ int check_common(int64_t M, int64_t N, int64_t K, int64_t G, int x_dtype) {
     return PW4_OK;
 }
 
+// ev: the call's armed timing events, taken by the entry point (they time the
+// GEMM kernel launches only, not the repack, gather, combine or SiLU passes).
 int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const void* scales, int stype,
              const uint32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N, int64_t K, int64_t G,
-             int64_t num_splits, void* workspace, size_t ws_bytes, hipStream_t stream, bool silu = false) {
+             int64_t num_splits, void* workspace, size_t ws_bytes, hipStream_t stream, KernelEvents ev,
+             bool silu = false) {
     // x and the weight words are read as 16-byte vectors
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) return PW4_ERR_ARG;
     const Plan p =
@@ -459,7 +473,7 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.ups = (int)ceil_div(a.ncg, p.dc.wps);
         a.spr_recip = (uint32_t)(((uint64_t{1} << 32) + (uint64_t)(p.dc.k_per_split / 8 + 1) - 1) /
                                  (uint64_t)(p.dc.k_per_split / 8 + 1));
-        e = launch_decode(layout, xt, stype, qzeros != nullptr, p.dc, a, stream);
+        e = launch_decode(layout, xt, stype, qzeros != nullptr, p.dc, a, stream, ev);
         if (e != hipSuccess) return hip_fail(e);
     } else {
         PrefillArgs a{};
@@ -483,8 +497,9 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.n_end = (int)N;
         a.cus = cu_count();
         a.tile_rows = p.p_tile_rows;
-        e = p.p256 ? launch_prefill256(xt, stype, qzeros != nullptr, a, stream)
-                   : launch_prefill(layout, xt, stype, qzeros != nullptr, a, stream);
+        a.exact = p.p_exact ? 1 : 0;
+        e = p.p256 ? launch_prefill256(xt, stype, qzeros != nullptr, a, stream, ev)
+                   : launch_prefill(layout, xt, stype, qzeros != nullptr, a, stream, ev);
         if (e != hipSuccess) return hip_fail(e);
     }
     if (p.use_partial && !p.decode) {
@@ -519,8 +534,7 @@ const char* pw4_last_hip_error(void) { return g_last_hip_error; }
 
 int pw4_time_next_kernel(void* start_event, void* stop_event) {
     if ((start_event == nullptr) != (stop_event == nullptr)) return PW4_ERR_ARG;
-    pw4::g_timing_start = static_cast<hipEvent_t>(start_event);
-    pw4::g_timing_stop = static_cast<hipEvent_t>(stop_event);
+    pw4::g_armed_events = {static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
     return PW4_OK;
 }
 
@@ -565,6 +579,7 @@ size_t pw4_gemm_w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int64_t gr
 int pw4_gemm_w4a16(const void* x, int x_dtype, const int32_t* weight_packed, const float* weight_scale, void* y,
                    int64_t M, int64_t N, int64_t K, int64_t group_size, int64_t num_splits, void* workspace,
                    size_t workspace_bytes, pw4_stream_t stream) {
+    const KernelEvents ev = take_kernel_events();
     int rc = check_common(M, N, K, group_size, x_dtype);
     if (rc != PW4_OK) return rc;
     if (num_splits < 0) return PW4_ERR_ARG;
@@ -572,7 +587,7 @@ int pw4_gemm_w4a16(const void* x, int x_dtype, const int32_t* weight_packed, con
     if (!x || !weight_packed || !weight_scale || !y) return PW4_ERR_ARG;
     return run_gemm(LAYOUT_CT, x, x_dtype, reinterpret_cast<const uint32_t*>(weight_packed), weight_scale, S_F32,
                     nullptr, nullptr, y, M, N, K, group_size, num_splits, workspace, workspace_bytes,
-                    reinterpret_cast<hipStream_t>(stream));
+                    reinterpret_cast<hipStream_t>(stream), ev);
 }
 
 size_t pw4_gemm_w4a16_marlin_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm,
@@ -587,6 +602,7 @@ int pw4_gemm_w4a16_marlin(const void* x, int x_dtype, const int32_t* weight_marl
                           int scale_dtype, const int32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N,
                           int64_t K, int64_t group_size, int64_t num_splits, void* workspace,
                           size_t workspace_bytes, pw4_stream_t stream) {
+    const KernelEvents ev = take_kernel_events();
     int rc = check_common(M, N, K, group_size, x_dtype);
     if (rc != PW4_OK) return rc;
     if (num_splits < 0) return PW4_ERR_ARG;
@@ -597,7 +613,7 @@ int pw4_gemm_w4a16_marlin(const void* x, int x_dtype, const int32_t* weight_marl
     return run_gemm(LAYOUT_MARLIN, x, x_dtype, reinterpret_cast<const uint32_t*>(weight_marlin), scales,
                     scale_dtype == PW4_DTYPE_F32 ? S_F32 : S_F16, reinterpret_cast<const uint32_t*>(qzeros), perm, y,
                     M, N, K, group_size, num_splits, workspace, workspace_bytes,
-                    reinterpret_cast<hipStream_t>(stream));
+                    reinterpret_cast<hipStream_t>(stream), ev);
 }
 
 size_t pw4_gemm_w4a16_silu_mul_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm) {
@@ -611,6 +627,7 @@ int pw4_gemm_w4a16_silu_mul(const void* x, int x_dtype, const int32_t* weight_ma
                             int scale_dtype, const int32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N,
                             int64_t K, int64_t group_size, void* workspace, size_t workspace_bytes,
                             pw4_stream_t stream) {
+    const KernelEvents ev = take_kernel_events();
     int rc = check_common(M, N, K, group_size, x_dtype);
     if (rc != PW4_OK) return rc;
     if (scale_dtype != PW4_DTYPE_F32 && scale_dtype != PW4_DTYPE_F16) return PW4_ERR_ARG;
@@ -619,7 +636,7 @@ int pw4_gemm_w4a16_silu_mul(const void* x, int x_dtype, const int32_t* weight_ma
     if (!x || !weight_marlin || !scales || !y) return PW4_ERR_ARG;
     return run_gemm(LAYOUT_MARLIN, x, x_dtype, reinterpret_cast<const uint32_t*>(weight_marlin), scales,
                     scale_dtype == PW4_DTYPE_F32 ? S_F32 : S_F16, reinterpret_cast<const uint32_t*>(qzeros), perm, y,
-                    M, N, K, group_size, 0, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream),
+                    M, N, K, group_size, 0, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream), ev,
                     /*silu=*/true);
 }
 

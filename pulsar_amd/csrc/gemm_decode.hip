@@ -42,8 +42,6 @@
 #include <tuple>
 #include <type_traits>
 
-#include <hip/hip_ext.h>
-
 #include "w4a16_common.h"
 #include "w4a16_kernels.h"
 
@@ -785,7 +783,7 @@ int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int 
 }
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
-                         hipStream_t stream) {
+                         hipStream_t stream, KernelEvents ev) {
     const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp, cfg.ring, cfg.tree);
     if (fn == nullptr) return hipErrorInvalidValue;
     // the kernel maps slots to rows with a multiply-high by spr_recip, exact
@@ -794,15 +792,7 @@ hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const Decode
     if (x_slots(a.M, a.k_per_split) * spr >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
     hipError_t e = prepare(fn, cfg.lds_bytes);
     if (e != hipSuccess) return e;
-    hipEvent_t t0 = nullptr, t1 = nullptr;
-    take_timing_events(&t0, &t1);
-    if (t0 != nullptr) {
-        // the events take this dispatch's own start and end timestamps
-        void* args[] = {const_cast<DecodeArgs*>(&a)};
-        return hipExtLaunchKernel(reinterpret_cast<const void*>(fn), dim3(a.wps, a.splits), dim3(kThreads), args,
-                                  cfg.lds_bytes, stream, t0, t1, 0);
-    }
-    hipLaunchKernelGGL(fn, dim3(a.wps, a.splits), dim3(kThreads), cfg.lds_bytes, stream, a);
+    launch_kernel(fn, dim3(a.wps, a.splits), dim3(kThreads), (uint32_t)cfg.lds_bytes, stream, ev.start, ev.stop, a);
     return hipGetLastError();
 }
 

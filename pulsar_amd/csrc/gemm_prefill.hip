@@ -293,9 +293,10 @@ __global__ __launch_bounds__(256) void gather_x_kernel(const uint16_t* __restric
 }
 
 template <bool BF16, int LAYOUT, typename ST, bool ZP>
-hipError_t launch_one(const PrefillArgs& a, hipStream_t stream) {
+hipError_t launch_one(const PrefillArgs& a, hipStream_t stream, KernelEvents ev) {
     const int nwg = (int)(ceil_div(a.M, BM) * ceil_div(a.N, BN));
-    hipLaunchKernelGGL((prefill_kernel<BF16, LAYOUT, ST, ZP>), dim3(nwg, 1, a.splits), dim3(kThreads), 0, stream, a);
+    launch_kernel(prefill_kernel<BF16, LAYOUT, ST, ZP>, dim3(nwg, 1, a.splits), dim3(kThreads), 0, stream, ev.start,
+                  ev.stop, a);
     return hipGetLastError();
 }
 
@@ -304,23 +305,24 @@ hipError_t launch_one(const PrefillArgs& a, hipStream_t stream) {
 int prefill_tile_m() { return BM; }
 int prefill_tile_n() { return BN; }
 
-hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream) {
+hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream,
+                          KernelEvents ev) {
     const bool bf = xtype == X_BF16;
     if (layout == LAYOUT_CT) {
         if (zp || stype != S_F32) return hipErrorInvalidValue;
-        return bf ? launch_one<true, LAYOUT_CT, float, false>(a, stream)
-                  : launch_one<false, LAYOUT_CT, float, false>(a, stream);
+        return bf ? launch_one<true, LAYOUT_CT, float, false>(a, stream, ev)
+                  : launch_one<false, LAYOUT_CT, float, false>(a, stream, ev);
     }
     if (stype == S_F32) {
-        if (zp) return bf ? launch_one<true, LAYOUT_MARLIN, float, true>(a, stream)
-                          : launch_one<false, LAYOUT_MARLIN, float, true>(a, stream);
-        return bf ? launch_one<true, LAYOUT_MARLIN, float, false>(a, stream)
-                  : launch_one<false, LAYOUT_MARLIN, float, false>(a, stream);
+        if (zp) return bf ? launch_one<true, LAYOUT_MARLIN, float, true>(a, stream, ev)
+                          : launch_one<false, LAYOUT_MARLIN, float, true>(a, stream, ev);
+        return bf ? launch_one<true, LAYOUT_MARLIN, float, false>(a, stream, ev)
+                  : launch_one<false, LAYOUT_MARLIN, float, false>(a, stream, ev);
     }
-    if (zp) return bf ? launch_one<true, LAYOUT_MARLIN, _Float16, true>(a, stream)
-                      : launch_one<false, LAYOUT_MARLIN, _Float16, true>(a, stream);
-    return bf ? launch_one<true, LAYOUT_MARLIN, _Float16, false>(a, stream)
-              : launch_one<false, LAYOUT_MARLIN, _Float16, false>(a, stream);
+    if (zp) return bf ? launch_one<true, LAYOUT_MARLIN, _Float16, true>(a, stream, ev)
+                      : launch_one<false, LAYOUT_MARLIN, _Float16, true>(a, stream, ev);
+    return bf ? launch_one<true, LAYOUT_MARLIN, _Float16, false>(a, stream, ev)
+              : launch_one<false, LAYOUT_MARLIN, _Float16, false>(a, stream, ev);
 }
 
 hipError_t launch_gather_x(const uint16_t* x, const int32_t* perm, uint16_t* out, int M, int K, hipStream_t stream) {

@@ -35,6 +35,16 @@
 // reference's bf16 fragment round(q * round(s)) bit for bit
 // (w4a16_marlin.cu:115-126).
 //
+// Exact scaling (fp16 x, 128-row tiles).  Rounding (u - z) * s to fp16 costs
+// up to 2^-11 of every weight; summed over K = 14336-28672 that is ~1e-2 of
+// absolute error at the BASELINE magnitudes.  In this mode B = u - z (exact in
+// fp16) and the group scale is applied in fp32 to the accumulators instead:
+// with s_g the scale of group g for the lane's column, the running sum is
+// rescaled by s_(g-1) / s_g when group g starts and multiplied by the last
+// group's scale at the end, so acc = sum_g s_g * P_g with P_g the exact
+// fp32 sum of group g.  One multiply per accumulator per group (the
+// accumulators are VGPRs here), and no second accumulator set.
+//
 // Reference counterpart: w4a16_marlin_kernel at BM = 64
 // (pulsar-core/src/kernels/w4a16_marlin.cu:197-304).
 #include <algorithm>
@@ -90,13 +100,24 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
+// Scales below this magnitude (zero included) count as this value, with their
+// sign, in exact mode: the group then contributes ~2^-64 of its sum instead of
+// nothing, and the ratio of two scales stays finite.
+constexpr float kMinScale = 0x1p-64f;
+
+__device__ __forceinline__ float exact_scale(float s) {
+    return __builtin_fabsf(s) < kMinScale ? __builtin_copysignf(kMinScale, s) : s;
+}
+
 // RT = 32-row MFMA tiles per wave: 8 (256-row tile) or 4 (128-row tile, for
-// the N columns of the last wave; see launch_prefill256).
+// the N columns of the last wave, every tile of a 128-row plan, and exact
+// scaling; see launch_prefill256).
 // 128-row tiles (RT = 4) use 78 KB of LDS, so two workgroups fit on a CU if
 // each wave keeps to 256 registers (two waves per SIMD).
-template <bool BF16, typename ST, bool ZP, bool PARTIAL, int RT>
+template <bool BF16, typename ST, bool ZP, bool PARTIAL, int RT, bool EXACT = false>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(RT == 4 ? 2 : 1, RT == 4 ? 2 : 1)))
 void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
+    static_assert(!EXACT || (!BF16 && RT == 4), "exact scaling: fp16 activations, 128-row tiles");
     constexpr int TMR = 32 * RT;                 // rows of this tile
     constexpr int kAStage = TMR * TK * 2;        // bytes
     __shared__ __attribute__((aligned(16))) uint8_t sA[kStages][kAStage];
@@ -177,11 +198,16 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
     uint32_t one;
     asm volatile("v_mov_b32 %0, %1" : "=v"(one) : "s"(BF16 ? 0x43004300u : 0x64006400u));
 
+    // exact mode: the effective scale of the group the accumulators are in,
+    // per column tile (1 until the first chunk; an empty slice stores 0 * 1)
+    float s_run[2] = {1.f, 1.f};
+
     // One chunk = four 16-K steps; step s is pair s % 2 of 32-K tile s / 2, and
     // this lane's K run in it is [16s + 8hb, +8): activation 16-byte unit
     // 2s + hb, weight nibble pair 2(s % 2) + hb.  Operands of step s + 1 (eight
     // A fragments, the dequantized B) are fetched while step s's 16 MFMAs run.
-    auto compute = [&](int st) {
+    // new_group (exact mode): this chunk starts a quant group after another one.
+    auto compute = [&](int st, bool new_group) {
         const uint8_t* A = &sA[st][0];
         const uint8_t* B = &sB[st][0] + wave * 2048;
         u32x4 wq[2][2];
@@ -205,6 +231,17 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
             if constexpr (BF16) {
                 sb[ct] = (float)(__bf16)sf;
                 cz[ct] = -(128.f + (float)z) * sb[ct];
+            } else if constexpr (EXACT) {
+                z2[ct] = as_h2((0x6400u | z) * 0x10001u);  // 1024 + z
+                const float se = exact_scale(sf);
+                if (new_group) {
+                    const float r = s_run[ct] / se;
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) acc[rt][ct][e] *= r;
+                }
+                s_run[ct] = se;
             } else {
                 const _Float16 sh = (_Float16)sf;
                 s2[ct] = f16x2{sh, sh};
@@ -230,6 +267,8 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
                         bv[ct][tg] = pack_bf16x2_rne(__builtin_fmaf(__builtin_bit_cast(float, v << 16), sb[ct], cz[ct]),
                                                      __builtin_fmaf(__builtin_bit_cast(float, v & 0xffff0000u), sb[ct],
                                                                     cz[ct]));
+                    } else if constexpr (EXACT) {
+                        bv[ct][tg] = as_u32(as_h2(v) - z2[ct]);  // u - z, exact
                     } else {
                         bv[ct][tg] = as_u32((as_h2(v) - z2[ct]) * s2[ct]);
                     }
@@ -268,6 +307,9 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
 
     if (nck > 0) issue(c_begin, 0);
     if (nck > 1) issue(c_begin + 1, 1);
+    // position of the chunk in its quant group (G is a multiple of 64)
+    const int cpg = a.G / TK;
+    int gk = EXACT ? c_begin % cpg : 0;
     for (int i = 0; i < nck; ++i) {
         const int st = i % kStages;
         if (i + 1 < nck) {
@@ -277,7 +319,16 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
         }
         __syncthreads();            // everyone's have; everyone is done with chunk i - 1
         if (i + 2 < nck) issue(c_begin + i + 2, (i + 2) % kStages);
-        compute(st);
+        compute(st, i > 0 && gk == 0);
+        if constexpr (EXACT) gk = gk + 1 == cpg ? 0 : gk + 1;
+    }
+    if constexpr (EXACT) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[rt][ct][e] *= s_run[ct];
     }
 
     // ---- epilogue: D lane holds column c, rows 8*(e/4) + 4*hb + e%4 ---------
@@ -395,28 +446,39 @@ int64_t prefill256_tail_cols(int64_t M, int64_t N, int cus, double* waves) {
 // work each, filling the last wave (qkv: 256 full tiles, then 256 half tiles).
 // Same arithmetic per output element, so the result does not change.
 template <bool BF16, typename ST, bool ZP>
-void launch_variant(const PrefillArgs& a, hipStream_t stream) {
+void launch_variant(const PrefillArgs& a, hipStream_t stream, KernelEvents ev) {
     const NibbleMasks mk{};
     const int64_t num_m = ceil_div(a.M, TM), num_n = ceil_div(a.N, TN);
+    const int64_t tiles128 = ceil_div(a.M, TM / 2) * num_n;  // 128-row tiles over every column
+    PrefillArgs w = a;  // a launch over every column of the output
+    w.n_begin = 0;
+    w.n_end = a.N;
+    if constexpr (!BF16) {
+        if (a.exact) {  // exact scaling: 128-row tiles only (the plan asks for no others)
+            const dim3 grid((unsigned)tiles128, 1, a.partial != nullptr ? a.splits : 1);
+            if (a.partial != nullptr) {
+                launch_kernel(prefill256_kernel<false, ST, ZP, true, 4, true>, grid, dim3(kT), 0, stream, ev.start,
+                              ev.stop, w, mk);
+            } else {
+                launch_kernel(prefill256_kernel<false, ST, ZP, false, 4, true>, grid, dim3(kT), 0, stream, ev.start,
+                              ev.stop, w, mk);
+            }
+            return;
+        }
+    }
     if (a.partial != nullptr) {  // K slices: fp32 partials of 256- or 128-row tiles
-        PrefillArgs f = a;
-        f.n_begin = 0;
-        f.n_end = a.N;
         if (a.tile_rows == TM / 2) {
-            hipLaunchKernelGGL((prefill256_kernel<BF16, ST, ZP, true, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * num_n), 1,
-                                                                          a.splits), dim3(kT), 0, stream, f, mk);
+            launch_kernel(prefill256_kernel<BF16, ST, ZP, true, 4>, dim3((unsigned)tiles128, 1, a.splits), dim3(kT), 0,
+                          stream, ev.start, ev.stop, w, mk);
         } else {
-            hipLaunchKernelGGL((prefill256_kernel<BF16, ST, ZP, true, 8>), dim3((unsigned)(num_m * num_n), 1, a.splits),
-                               dim3(kT), 0, stream, f, mk);
+            launch_kernel(prefill256_kernel<BF16, ST, ZP, true, 8>, dim3((unsigned)(num_m * num_n), 1, a.splits),
+                          dim3(kT), 0, stream, ev.start, ev.stop, w, mk);
         }
         return;
     }
     if (a.tile_rows == TM / 2) {  // every tile 128 rows: twice the workgroups, two per CU
-        PrefillArgs h = a;
-        h.n_begin = 0;
-        h.n_end = a.N;
-        hipLaunchKernelGGL((prefill256_kernel<BF16, ST, ZP, false, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * num_n)),
-                           dim3(kT), 0, stream, h, mk);
+        launch_kernel(prefill256_kernel<BF16, ST, ZP, false, 4>, dim3((unsigned)tiles128), dim3(kT), 0, stream,
+                      ev.start, ev.stop, w, mk);
         return;
     }
     const int64_t nt = prefill256_tail_cols(a.M, a.N, a.cus, nullptr);
@@ -425,29 +487,29 @@ void launch_variant(const PrefillArgs& a, hipStream_t stream) {
         PrefillArgs f = a;
         f.n_begin = 0;
         f.n_end = (int)std::min<int64_t>(a.N, nfull * TN);
-        hipLaunchKernelGGL((prefill256_kernel<BF16, ST, ZP, false, 8>), dim3((unsigned)(num_m * nfull)), dim3(kT), 0, stream,
-                           f, mk);
+        launch_kernel(prefill256_kernel<BF16, ST, ZP, false, 8>, dim3((unsigned)(num_m * nfull)), dim3(kT), 0, stream,
+                      ev.start, nt > 0 ? nullptr : ev.stop, f, mk);
     }
     if (nt > 0) {
         PrefillArgs h = a;
         h.n_begin = (int)(nfull * TN);
         h.n_end = a.N;
-        hipLaunchKernelGGL((prefill256_kernel<BF16, ST, ZP, false, 4>), dim3((unsigned)(ceil_div(a.M, TM / 2) * nt)), dim3(kT),
-                           0, stream, h, mk);
+        launch_kernel(prefill256_kernel<BF16, ST, ZP, false, 4>, dim3((unsigned)(ceil_div(a.M, TM / 2) * nt)), dim3(kT),
+                      0, stream, nfull > 0 ? nullptr : ev.start, ev.stop, h, mk);
     }
 }
 
 template <bool BF16>
-void launch_dtype(int stype, bool zp, const PrefillArgs& a, hipStream_t stream) {
+void launch_dtype(int stype, bool zp, const PrefillArgs& a, hipStream_t stream, KernelEvents ev) {
     if (stype == S_F32) {
-        zp ? launch_variant<BF16, float, true>(a, stream) : launch_variant<BF16, float, false>(a, stream);
+        zp ? launch_variant<BF16, float, true>(a, stream, ev) : launch_variant<BF16, float, false>(a, stream, ev);
     } else {
-        zp ? launch_variant<BF16, _Float16, true>(a, stream) : launch_variant<BF16, _Float16, false>(a, stream);
+        zp ? launch_variant<BF16, _Float16, true>(a, stream, ev) : launch_variant<BF16, _Float16, false>(a, stream, ev);
     }
 }
 
-hipError_t launch_prefill256(int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream) {
-    xtype == X_BF16 ? launch_dtype<true>(stype, zp, a, stream) : launch_dtype<false>(stype, zp, a, stream);
+hipError_t launch_prefill256(int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream, KernelEvents ev) {
+    xtype == X_BF16 ? launch_dtype<true>(stype, zp, a, stream, ev) : launch_dtype<false>(stype, zp, a, stream, ev);
     return hipGetLastError();
 }
 

@@ -12,6 +12,7 @@
 
 #include <map>
 #include <mutex>
+#include <vector>
 
 #include "pulsar_w4a16.h"
 
@@ -39,23 +40,48 @@ void check_status(int rc, const char* op) {
 
 int x_dtype_code(const at::Tensor& x) { return x.scalar_type() == at::kBFloat16 ? PW4_DTYPE_BF16 : PW4_DTYPE_F16; }
 
-// GEMM workspace: one per (device, stream), zero-filled when it is
-// allocated or grown, then reused.  The C ABI needs the counter region at its
-// start to be zero on entry and leaves it zero, and calls on one stream are
-// ordered, so sharing one workspace per stream is race free.
+// GEMM workspaces: one per (device, stream).  The C ABI needs the zero region
+// at the start of a workspace to be zero on entry and leaves it zero, and
+// calls on one stream are ordered, so the calls of a stream share one buffer.
+// Under HIP graph capture three rules keep that true:
+//  * a buffer is never freed.  When a call needs more, the smaller buffer is
+//    retired but kept alive until the process exits, so a graph that captured
+//    its address still replays into valid memory that nothing else uses;
+//  * a buffer allocated while the stream captures is zeroed by a fill node of
+//    the graph (at::zeros records one), so a replay zeroes it before the GEMM.
+//    That fill never ran eagerly: the next eager call on the stream zeroes
+//    the buffer first, and the next capture records a fill of its own;
+//  * graphs captured on one stream share that stream's buffer, so they are
+//    replayed in order (on one stream, or synchronised), like the calls of a
+//    stream.
+struct StreamWorkspace {
+    at::Tensor buf;
+    bool zeroed_eagerly = true;  // false until a buffer allocated under capture is zeroed outside it
+};
+
 at::Tensor workspace(size_t bytes, const at::Tensor& like) {
     if (bytes == 0) return at::Tensor();
     static std::mutex mu;
-    static std::map<std::pair<int64_t, int64_t>, at::Tensor> cache;
+    static std::map<std::pair<int64_t, int64_t>, StreamWorkspace> cache;
+    static std::vector<at::Tensor> retired;
     const auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA();
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    TORCH_CHECK(hipStreamIsCapturing(stream.stream(), &cs) == hipSuccess,
+                "W4A16 workspace: hipStreamIsCapturing failed");
+    const bool capturing = cs != hipStreamCaptureStatusNone;
     const std::pair<int64_t, int64_t> key{like.device().index(), (int64_t)stream.id()};
     std::lock_guard<std::mutex> lock(mu);
-    at::Tensor& t = cache[key];
-    if (!t.defined() || (size_t)t.numel() < bytes) {
-        const size_t grow = t.defined() ? std::max(bytes, (size_t)t.numel() * 2) : bytes;
-        t = at::zeros({(int64_t)grow}, like.options().dtype(at::kByte));
+    StreamWorkspace& w = cache[key];
+    if (!w.buf.defined() || (size_t)w.buf.numel() < bytes) {
+        const size_t grow = w.buf.defined() ? std::max(bytes, (size_t)w.buf.numel() * 2) : bytes;
+        if (w.buf.defined()) retired.push_back(std::move(w.buf));
+        w.buf = at::zeros({(int64_t)grow}, like.options().dtype(at::kByte));
+        w.zeroed_eagerly = !capturing;
+    } else if (!w.zeroed_eagerly) {
+        w.buf.zero_();  // eagerly, or as a fill node of this capture too
+        w.zeroed_eagerly = !capturing;
     }
-    return t;
+    return w.buf;
 }
 
 void* ptr_or_null(const at::Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }

@@ -2,10 +2,34 @@
 // kernel translation units.  Not part of the public header.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace pw4 {
+
+// Events that take one GEMM call's kernel timestamps (pw4_time_next_kernel):
+// `start` the start of the call's first GEMM dispatch, `stop` the end of its
+// last (a split-K combine or SiLU pass after it is not included).  Null: none.
+struct KernelEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+
+// The events armed on the calling thread, which are disarmed: every GEMM entry
+// point takes them first, so they never outlive the call they were armed for.
+KernelEvents take_kernel_events();
+
+// hipLaunchKernelGGL, or hipExtLaunchKernelGGL when an event is given (that
+// launch path costs the runtime more, so untimed launches do not take it).
+template <typename F, typename... Args>
+void launch_kernel(F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t stream, hipEvent_t start,
+                   hipEvent_t stop, Args... args) {
+    if (start != nullptr || stop != nullptr) {
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, start, stop, 0, args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+    }
+}
 
 enum XType : int { X_F16 = 0, X_BF16 = 1 };
 enum SType : int { S_F32 = 0, S_F16 = 1 };
@@ -79,12 +103,8 @@ int decode_threads();
 int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree,
                          size_t lds);
 
-// Events armed on the calling thread by pw4_time_next_kernel for its next
-// decode-kernel launch; returns them (nulls when none) and disarms.
-void take_timing_events(hipEvent_t* start, hipEvent_t* stop);
-
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
-                         hipStream_t stream);
+                         hipStream_t stream, KernelEvents ev = {});
 hipError_t launch_combine(const float* partial, uint16_t* y, int64_t mn, int splits, int xtype, hipStream_t stream);
 // The same fixed-order sum over [splits, M, N] partials of gate|up interleaved
 // columns (N % 16 == 0), writing y [M, N/2] = silu(gate) * up.
@@ -111,9 +131,12 @@ struct PrefillArgs {
     int cus;                 // compute units of the device (tail balancing)
     int tile_rows;           // 256-wide kernel: 256-row tiles (tail balanced when unsplit) or 128-row tiles
     int silu;                // 256-wide kernel, unsplit: y [M, N/2] = silu(gate) * up (see DecodeArgs)
+    int exact;               // 256-wide kernel, fp16 x: B = u - z and the scale applied to the fp32
+                             // accumulators per group (128-row tiles only)
 };
 
-hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream);
+hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream,
+                          KernelEvents ev = {});
 int prefill_tile_m();
 int prefill_tile_n();
 
@@ -124,7 +147,8 @@ int prefill256_tile();
 // Unsplit 256-row launches: N-tile columns run as 128-row tail tiles, and the
 // launch's cost in waves of full tiles (into *waves when not null).
 int64_t prefill256_tail_cols(int64_t M, int64_t N, int cus, double* waves);
-hipError_t launch_prefill256(int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream);
+hipError_t launch_prefill256(int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream,
+                             KernelEvents ev = {});
 
 // x_out[m, j] = x[m, perm[j]]
 hipError_t launch_gather_x(const uint16_t* x, const int32_t* perm, uint16_t* out, int M, int K, hipStream_t stream);

@@ -5,6 +5,10 @@ prefill shapes only a seeded subset of output rows is recomputed on the CPU:
 rows of y = x @ W^T are independent, so the subset check is exact for those
 rows, and a checksum of the whole output (column sums of y against
 (1^T x) @ W^T over the same oracle) covers every row.
+
+Every case is held to all three fp16 bars of the north star (rel-L2 <= 1e-3,
+max-abs <= 1e-2 beyond the fp16 output's own rounding, and the reference's
+max-relative bar); the measured figures are printed for the record.
 """
 
 import numpy as np
@@ -40,12 +44,11 @@ def test_prefill_llama8b_rows(layer, m):
     c = baseline_case(m, n, k, 128, seed=0, rows=rows)
     wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float16), 128)
     y = ops.gemm_w4a16_marlin(c.x, wm, sm, 128)
-    r = check(y[torch.from_numpy(rows).cuda()], c.y_ref, torch.float16, f"prefill {layer} m={m}",
-              abs_excess=False)
+    r = check(y[torch.from_numpy(rows).cuda()], c.y_ref, torch.float16, f"prefill {layer} m={m}")
     print(f"prefill {layer} m={m}: {r}")
 
 
-@pytest.mark.parametrize("layer", ["qkv", "down"])
+@pytest.mark.parametrize("layer", list(LLAMA70B))
 @pytest.mark.parametrize("m", [1, 16, 2048])
 def test_act_order_llama70b(layer, m):
     k, n = LLAMA70B[layer]
@@ -56,14 +59,16 @@ def test_act_order_llama70b(layer, m):
     y = ops.gemm_w4a16_gptq(c.x, wm, scales, c.qzeros(), perm, 128)
     if rows is not None:
         y = y[torch.from_numpy(rows).cuda()]
-    r = check(y, c.y_ref, torch.float16, f"act-order {layer} m={m}", abs_excess=m <= 16)
+    r = check(y, c.y_ref, torch.float16, f"act-order {layer} m={m}")
     print(f"act-order 70B {layer} m={m}: {r}")
 
 
-def test_output_checksum_prefill():
+@pytest.mark.parametrize("layer", ["o", "gate_up", "down"])
+def test_output_checksum_prefill(layer):
     """Column sums of y over ALL rows against the oracle: sum_m y[m, :] equals
     (sum_m x[m, :]) @ W^T up to fp16 output rounding of each term."""
-    m, k, n = 4096, 4096, 4096
+    k, n = LLAMA8B[layer]
+    m = 4096
     p = O.make_problem(m, n, k, 128, seed=2)
     w = p.dequant()
     colsum_ref = O.gemm_f32(np.ascontiguousarray(p.xf.sum(axis=0, keepdims=True)), w)[0]
@@ -73,4 +78,5 @@ def test_output_checksum_prefill():
     y = ops.gemm_w4a16_marlin(c_x, wm, sm, 128)
     colsum = y.float().sum(dim=0).cpu().numpy()
     r = metrics(torch.from_numpy(colsum), colsum_ref)
+    print(f"checksum {layer} m={m}: {r}")
     assert r["rel_l2"] < 1e-3, r

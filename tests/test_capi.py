@@ -13,6 +13,7 @@ import torch
 
 import pulsar_amd
 from pulsar_amd import ops
+from pw4_capi import declare
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "pulsar_w4a16.h")
@@ -23,35 +24,7 @@ I64 = ctypes.c_int64
 
 @pytest.fixture(scope="module")
 def lib():
-    L = pulsar_amd.capi()
-    L.pw4_status_string.restype = ctypes.c_char_p
-    L.pw4_status_string.argtypes = [ctypes.c_int]
-    L.pw4_marlin_words.restype = I64
-    L.pw4_marlin_words.argtypes = [I64, I64]
-    L.pw4_gemm_w4a16.restype = ctypes.c_int
-    L.pw4_gemm_w4a16.argtypes = [P, ctypes.c_int, P, P, P, I64, I64, I64, I64, I64, P, ctypes.c_size_t, P]
-    L.pw4_gemm_w4a16_marlin.restype = ctypes.c_int
-    L.pw4_gemm_w4a16_marlin.argtypes = [P, ctypes.c_int, P, P, ctypes.c_int, P, P, P, I64, I64, I64, I64, I64, P,
-                                        ctypes.c_size_t, P]
-    L.pw4_gemm_w4a16_workspace_size.restype = ctypes.c_size_t
-    L.pw4_gemm_w4a16_workspace_size.argtypes = [I64, I64, I64, I64, I64]
-    L.pw4_gemm_w4a16_marlin_workspace_size.restype = ctypes.c_size_t
-    L.pw4_gemm_w4a16_marlin_workspace_size.argtypes = [I64, I64, I64, I64, ctypes.c_int, I64]
-    L.pw4_gemm_w4a16_silu_mul.restype = ctypes.c_int
-    L.pw4_gemm_w4a16_silu_mul.argtypes = [P, ctypes.c_int, P, P, ctypes.c_int, P, P, P, I64, I64, I64, I64, P,
-                                          ctypes.c_size_t, P]
-    L.pw4_gemm_w4a16_silu_mul_workspace_size.restype = ctypes.c_size_t
-    L.pw4_gemm_w4a16_silu_mul_workspace_size.argtypes = [I64, I64, I64, I64, ctypes.c_int]
-    L.pw4_repack_w4a16.restype = ctypes.c_int
-    L.pw4_repack_w4a16.argtypes = [P, P, ctypes.c_int, I64, I64, I64, P, P, P]
-    L.pw4_gidx_to_perm.restype = ctypes.c_int
-    L.pw4_gidx_to_perm.argtypes = [P, I64, I64, P, P, P]
-    L.pw4_repack_gptq.restype = ctypes.c_int
-    L.pw4_repack_gptq.argtypes = [P, P, I64, I64, P, P]
-    L.pw4_abi_version.restype = ctypes.c_int
-    L.pw4_time_next_kernel.restype = ctypes.c_int
-    L.pw4_time_next_kernel.argtypes = [P, P]
-    return L
+    return declare(pulsar_amd.capi())
 
 
 def declared_functions():

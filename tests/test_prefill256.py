@@ -64,7 +64,7 @@ def test_prefill_gptq(tile, sym, act, sdtype):
 
 @pytest.fixture
 def plan_env():
-    keys = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS")
+    keys = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS", "PW4_PREFILL_EXACT")
     old = {k: os.environ.get(k) for k in keys}
     yield os.environ
     for k, v in old.items():
@@ -103,16 +103,20 @@ def test_prefill_tail_split(plan_env):
     check(y, c.y_ref, torch.float16, "tail split m=1024 n=18432")
 
 
+@pytest.mark.parametrize("exact", ["1", "0"], ids=["exact", "rounded"])
 @pytest.mark.parametrize("rows", [256, 128])
 @pytest.mark.parametrize("splits", [1, 3, 8])
 @pytest.mark.parametrize("m,n", [(300, 520), (129, 264)])
-def test_prefill_plans_agree_with_oracle(plan_env, rows, splits, m, n):
+def test_prefill_plans_agree_with_oracle(plan_env, exact, rows, splits, m, n):
     """Every plan the 256-wide kernel can be given -- 256- or 128-row tiles,
-    unsplit (with 128-row tail tiles) or with K slices -- computes the same
-    GEMM: ragged M and N against the oracle, fp16 and fp32 scales."""
+    unsplit (with 128-row tail tiles) or with K slices, exact scaling (the
+    default for fp16 x, 128-row tiles whatever the override) or the scale
+    rounded into the fp16 B fragment -- computes the same GEMM: ragged M and N
+    against the oracle, fp16 and fp32 scales."""
     k, g = 1024, 128
     plan_env["PW4_PREFILL_ROWS"] = str(rows)
     plan_env["PW4_PREFILL_SPLITS"] = str(splits)
+    plan_env["PW4_PREFILL_EXACT"] = exact
     c = reference_case(m, n, k, g, torch.float16, seed=16)
     wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float16), g)
     y32 = ops.gemm_w4a16_marlin(c.x, wm, sm, g)

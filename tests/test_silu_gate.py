@@ -92,19 +92,21 @@ def plan_env():
 
 # (m, n = 2F, k, x dtype, plan overrides, absolute bound).  The absolute bound (max
 # error within half an fp16 ulp + 1e-2) holds where both GEMM outputs are exact fp32 sums of
-# exact q * s products and the gate is fused: the decode kernel's direct store.  The prefill
-# kernels round q * s to fp16 in the B fragment (as the reference's MMA path does), gated-after
-# plans round gate and up to fp16 first, and the product scales either error by the other
-# factor; those cases are held to the relative bounds (rel-L2 1e-3, max 5e-3 of max |y|).
+# exact (u - z) * s products and the gate is applied to them in fp32: the decode kernel's
+# direct store, and the 256-wide prefill kernel with fp16 x (exact scaling) whether it gates in
+# its epilogue or in the split-K combine.  The 128 x 128 kernel and the bf16 path round q * s to
+# 16 bits in the B fragment (as the reference's MMA path does), gated-after plans round gate
+# and up to fp16 first, and the product scales either error by the other factor; those cases
+# are held to the relative bounds (rel-L2 1e-3, max 5e-3 of max |y|).
 CASES = [
     (1, 512, 512, torch.float16, {}, True),      # decode, direct store
     (16, 1024, 1024, torch.float16, {}, True),
     (5, 4160, 256, torch.float16, {}, True),     # N past a 64-column block boundary
     (24, 512, 4096, torch.float16, {}, False),   # decode, exchange-tree K slices
     (48, 256, 4096, torch.float16, {}, False),   # decode, counter K slices (M > 32)
-    (300, 1024, 512, torch.float16, {"PW4_PREFILL_SPLITS": "1"}, False),   # 256-wide prefill, unsplit
+    (300, 1024, 512, torch.float16, {"PW4_PREFILL_SPLITS": "1"}, True),    # 256-wide prefill, unsplit
     (200, 1024, 512, torch.bfloat16, {"PW4_PREFILL_SPLITS": "1"}, False),  # the same, bf16 x
-    (129, 512, 2048, torch.float16, {"PW4_PREFILL_SPLITS": "4"}, False),   # 256-wide, K slices -> combine
+    (129, 512, 2048, torch.float16, {"PW4_PREFILL_SPLITS": "4"}, True),    # 256-wide, K slices -> combine
     (100, 512, 4096, torch.bfloat16, {"PW4_PREFILL_TILE": "128"}, False),  # 128 x 128 kernel, K slices
     (700, 1024, 256, torch.float16, {"PW4_PREFILL_TILE": "128"}, False),   # 128 x 128 kernel, unsplit
 ]
