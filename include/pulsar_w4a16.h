@@ -139,6 +139,25 @@ int pw4_gemm_w4a16_marlin(const void* x, int x_dtype, const int32_t* weight_marl
                           size_t workspace_bytes, pw4_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * gemm_w4a16_marlin_noalloc: pw4_gemm_w4a16_marlin without a workspace
+ * argument.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, results and errors as
+ * pw4_gemm_w4a16_marlin, whose kernels it runs; it allocates nothing.  Its
+ * workspace is a fixed array of PW4_NOALLOC_SCRATCH_BYTES in the library's
+ * device code (one per device, held until the process exits); a call whose
+ * plan needs more returns PW4_ERR_WORKSPACE before launching anything (an
+ * automatic prefill plan whose K-slice partials would not fit runs unsplit
+ * instead).  The first call on a device clears the array's zero region with a
+ * fill kernel on `stream`; every call leaves it zero.  All calls on one device
+ * share the array: calls that overlap in time on one device (different
+ * streams, or host threads without ordering) race and give wrong results. */
+#define PW4_NOALLOC_SCRATCH_BYTES (64u << 20)
+int pw4_gemm_w4a16_marlin_noalloc(const void* x, int x_dtype, const int32_t* weight_marlin, const void* scales,
+                                  int scale_dtype, const int32_t* qzeros, const int32_t* perm, void* y, int64_t M,
+                                  int64_t N, int64_t K, int64_t group_size, int64_t num_splits, pw4_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * gemm_w4a16_silu_mul: the SwiGLU gate of the MLP in one call,
  *   y [M, N/2] = silu(x @ Wg^T) * (x @ Wu^T),
  * replacing the reference's two at::linear calls on gate_proj and up_proj and

@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "w4a16_common.h"
 #include "w4a16_kernels.h"
@@ -125,8 +126,9 @@ bool prefill_exact_enabled() {
     return !(e && e[0] == '0');
 }
 
-// only128: 128-row tiles only (the exact-scaling kernel has no 256-row variant)
-Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, bool only128) {
+// only128: 128-row tiles only (the exact-scaling kernel has no 256-row variant);
+// max_splits: the most K slices the plan may use.
+Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, bool only128, int64_t max_splits) {
     constexpr double kChunkUs = 2.0, kHalfChunk = 0.6, kShare = 0.8, kPartialBps = 6.0e12, kCombineUs = 2.0;
     Prefill256Plan best{256, 1};
     double best_us = 0.0;
@@ -135,7 +137,7 @@ Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, b
     for (int rows : {256, 128}) {
         if (only128 && rows != 128) continue;
         for (int64_t s : {1, 2, 3, 4, 6, 8}) {
-            if (s > nchunks) break;
+            if (s > nchunks || s > max_splits) break;
             const int64_t cps = ceil_div(nchunks, s);
             const int64_t sl = ceil_div(nchunks, cps);
             if (s > 1 && sl != s) continue;  // the same plan as a smaller s
@@ -185,8 +187,11 @@ struct Plan {
 };
 
 // layout: LAYOUT_MARLIN or LAYOUT_CT.  num_splits: 0 auto, >= 1 forced.
+// ws_cap: 0, or the most workspace bytes the caller has (the no-alloc entry
+// point's scratch): an automatic prefill plan whose K-slice partials would
+// not fit it runs unsplit instead.
 Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N, int64_t K, int64_t G, bool has_perm,
-               int64_t num_splits, bool silu = false) {
+               int64_t num_splits, bool silu = false, size_t ws_cap = 0) {
     Plan p;
     const int cus = cu_count();
     const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
@@ -349,13 +354,21 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         const int64_t base = ceil_div(M, tm) * ceil_div(N, tn);
         // K slices fill the chip when the tiles do not, but each costs an fp32
         // partial round trip of the output: keep at least 16 chunks per slice.
+        // does a plan of sl slices fit ws_cap (when there is one)?
+        auto fits = [&](int64_t sl) {
+            if (ws_cap == 0 || sl <= 1) return true;
+            const size_t need = kZeroRegion + align_up((size_t)sl * M * N * 4) +
+                                align_up(has_perm ? (size_t)M * K * 2 : 0) + align_up(p.repack_bytes);
+            return need <= ws_cap;
+        };
         int64_t s;
         if (forced) {
             s = std::min<int64_t>(num_splits, std::max<int64_t>(nchunks, 1));  // more would be empty slices
         } else if (p.p256 && prefill_splits_override()) {
             s = std::min<int64_t>(prefill_splits_override(), std::max<int64_t>(nchunks, 1));
         } else if (p.p256) {
-            const Prefill256Plan pp = plan_prefill256(M, N, nchunks, cus, p.p_exact);
+            Prefill256Plan pp = plan_prefill256(M, N, nchunks, cus, p.p_exact, 8);
+            if (!fits(pp.splits)) pp = plan_prefill256(M, N, nchunks, cus, p.p_exact, 1);
             s = pp.splits;
             p.p_tile_rows = pp.rows;
         } else if (base >= cus || nchunks < 8) {
@@ -363,6 +376,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         } else {
             s = std::min<int64_t>(ceil_div(cus, std::max<int64_t>(base, 1)), p.p256 ? nchunks / 16 : nchunks / 4);
             s = std::max<int64_t>(s, 1);
+            if (!fits(s)) s = 1;
         }
         int64_t cps = std::max<int64_t>(ceil_div(std::max<int64_t>(nchunks, 1), s), 1);
         if (!forced) s = std::max<int64_t>(ceil_div(nchunks, cps), 1);
@@ -401,11 +415,11 @@ int check_common(int64_t M, int64_t N, int64_t K, int64_t G, int x_dtype) {
 int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const void* scales, int stype,
              const uint32_t* qzeros, const int32_t* perm, void* y, int64_t M, int64_t N, int64_t K, int64_t G,
              int64_t num_splits, void* workspace, size_t ws_bytes, hipStream_t stream, KernelEvents ev,
-             bool silu = false) {
+             bool silu = false, size_t ws_cap = 0) {
     // x and the weight words are read as 16-byte vectors
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) return PW4_ERR_ARG;
-    const Plan p =
-        make_plan(layout, x_dtype, stype, qzeros != nullptr, M, N, K, G, perm != nullptr, num_splits, silu);
+    const Plan p = make_plan(layout, x_dtype, stype, qzeros != nullptr, M, N, K, G, perm != nullptr, num_splits, silu,
+                             ws_cap);
     if (p.workspace() > 0 && (workspace == nullptr || ws_bytes < p.workspace())) return PW4_ERR_WORKSPACE;
     char* ws = reinterpret_cast<char*>(workspace);
     int32_t* counters = p.workspace() ? reinterpret_cast<int32_t*>(ws) : nullptr;
@@ -514,6 +528,62 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
     return PW4_OK;
 }
 
+// ---- the no-alloc entry point's scratch -------------------------------------
+// One array per device (each GPU the library runs on holds its own copy until
+// the process exits).  Host code never names it directly: in host code the
+// symbol is a stand-in, not a device address, so its address on each device
+// comes from hipGetSymbolAddress once, with that device current.  Its first
+// PW4_ZERO_REGION_BYTES are the zero region of a workspace; the rest is
+// scratch (partials, the act-order copy of x, SiLU staging).
+constexpr size_t kStaticScratchBytes = PW4_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+__global__ __launch_bounds__(256) void zero_fill_kernel(u32x4* __restrict__ p, int64_t n16) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n16) p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+struct DeviceScratch {
+    void* ptr = nullptr;    // this device's copy of `scratch`
+    bool cleared = false;   // its zero region was cleared by a fill that ran (not one only recorded into a graph)
+};
+std::mutex g_scratch_mu;
+DeviceScratch g_scratch[kMaxDevices];
+
+// The current device's scratch, set up on the first call on that device: its
+// address, then a fill of the zero region on the caller's stream (a fill
+// kernel, not a memset, so that a capturing caller's graph can hold it).  A
+// fill only recorded into a graph has not run, so the next call from a stream
+// that is not capturing fills again; after that the GEMM kernels keep the
+// region zero.
+int device_scratch(hipStream_t stream, void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e);
+    if (dev < 0 || dev >= kMaxDevices) return PW4_ERR_ARG;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    DeviceScratch& d = g_scratch[dev];
+    if (d.ptr == nullptr) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e);
+        d.ptr = ptr;
+    }
+    if (!d.cleared) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &cs);
+        if (e != hipSuccess) return hip_fail(e);
+        const int64_t n16 = (int64_t)(kZeroRegion / 16);
+        hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)ceil_div(n16, 256)), dim3(256), 0, stream,
+                           reinterpret_cast<u32x4*>(d.ptr), n16);
+        e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(e);
+        d.cleared = cs == hipStreamCaptureStatusNone;
+    }
+    *out = d.ptr;
+    return PW4_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -614,6 +684,35 @@ int pw4_gemm_w4a16_marlin(const void* x, int x_dtype, const int32_t* weight_marl
                     scale_dtype == PW4_DTYPE_F32 ? S_F32 : S_F16, reinterpret_cast<const uint32_t*>(qzeros), perm, y,
                     M, N, K, group_size, num_splits, workspace, workspace_bytes,
                     reinterpret_cast<hipStream_t>(stream), ev);
+}
+
+int pw4_gemm_w4a16_marlin_noalloc(const void* x, int x_dtype, const int32_t* weight_marlin, const void* scales,
+                                  int scale_dtype, const int32_t* qzeros, const int32_t* perm, void* y, int64_t M,
+                                  int64_t N, int64_t K, int64_t group_size, int64_t num_splits, pw4_stream_t stream) {
+    const KernelEvents ev = take_kernel_events();
+    int rc = check_common(M, N, K, group_size, x_dtype);
+    if (rc != PW4_OK) return rc;
+    if (num_splits < 0) return PW4_ERR_ARG;
+    if (scale_dtype != PW4_DTYPE_F32 && scale_dtype != PW4_DTYPE_F16) return PW4_ERR_ARG;
+    if (qzeros && N % 8 != 0) return PW4_ERR_SHAPE;
+    if (M == 0 || N == 0) return PW4_OK;
+    if (!x || !weight_marlin || !scales || !y) return PW4_ERR_ARG;
+    // the plan run_gemm will make, sized before anything is launched
+    const size_t need = make_plan(LAYOUT_MARLIN, x_dtype, scale_dtype == PW4_DTYPE_F32 ? S_F32 : S_F16,
+                                  qzeros != nullptr, M, N, K, group_size, perm != nullptr, num_splits, false,
+                                  kStaticScratchBytes)
+                            .workspace();
+    if (need > kStaticScratchBytes) return PW4_ERR_WORKSPACE;
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    void* ws = nullptr;
+    if (need > 0) {
+        rc = device_scratch(s, &ws);
+        if (rc != PW4_OK) return rc;
+    }
+    return run_gemm(LAYOUT_MARLIN, x, x_dtype, reinterpret_cast<const uint32_t*>(weight_marlin), scales,
+                    scale_dtype == PW4_DTYPE_F32 ? S_F32 : S_F16, reinterpret_cast<const uint32_t*>(qzeros), perm, y,
+                    M, N, K, group_size, num_splits, ws, need > 0 ? kStaticScratchBytes : 0, s, ev, false,
+                    kStaticScratchBytes);
 }
 
 size_t pw4_gemm_w4a16_silu_mul_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm) {

@@ -14,6 +14,7 @@ SZ = ctypes.c_size_t
 INT = ctypes.c_int
 
 PW4_ZERO_REGION_BYTES = 16 << 20
+PW4_NOALLOC_SCRATCH_BYTES = 64 << 20
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 
 
@@ -33,6 +34,7 @@ def declare(L: ctypes.CDLL) -> ctypes.CDLL:
         "pw4_repack_gptq": (INT, [P, P, I64, I64, P, P]),
         "pw4_abi_version": (INT, []),
         "pw4_time_next_kernel": (INT, [P, P]),
+        "pw4_gemm_w4a16_marlin_noalloc": (INT, [P, INT, P, P, INT, P, P, P, I64, I64, I64, I64, I64, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
