@@ -21,8 +21,10 @@ Algorithmic bytes per GEMM: N*K/2 (int4) + N*(K/G)*2 (fp16 scales) +
 M*K*2 (x) + M*N*2 (y).
 
 MALL.  MI355X's 256 MB Infinity Cache would hold any one decode layer, so
-each layer has C distinct weight copies; with R = 4 and C = 8 a copy is
-reused only after ~850 MB of other weights have streamed through.
+each layer has C distinct weight copies holding >= 512 MB (8 for gate_up,
+60 for o).  In the graphs (R = 4) a copy is reused only after ~850 MB of other
+weights have streamed through; the roofline's single launches walk each
+layer's copies in turn, so every launch reads its weights from HBM.
 
 Also reported:
   reference_api = the same sweep through the reference's API
@@ -38,7 +40,12 @@ Also reported:
                   (BASELINE configs[3]) at M = 1, 16 (GB/s) and 2048 (TFLOP/s);
   cpu_baseline  = the reference CPU path (dequantize to fp32, fp32 GEMM --
                   the reference test oracle restated in oracle/) on this
-                  host's cores over a bounded sample of the sweep.
+                  host's cores over bounded samples of every config;
+  roofline.copy_ceiling / read_ceiling = a 512 MiB device copy and 1 GiB
+                  read-only reductions: what HBM gives a simple stream;
+  prefill_dense_fp16_yardstick = the dense fp16 library GEMM (hipBLASLt
+                  through torch) at the M = 4096 shapes;
+  repack        = repack_w4a16 per layer, GB/s of words and scales moved.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-prefill] [--no-cpu]
 """
@@ -65,8 +72,15 @@ PREFILL_M = [256, 1024, 4096]
 STACK_LAYERS = 32
 STACK_M = [1, 32]
 G = 128
-COPIES = 8
+COPIES = 8          # at least this many weight copies per layer
+MALL_SAFE_BYTES = 512 << 20  # ... and enough that one layer's copies hold this much (the MALL is 256 MB)
 REPS = 4
+
+
+def copies_for(k: int, n: int) -> int:
+    """Weight copies of one layer: rotating over them, a launch's weights were last
+    read >= 512 MB of that layer's own traffic earlier, so they come from HBM."""
+    return max(COPIES, -(-MALL_SAFE_BYTES // decode_bytes(1, k, n)))
 
 
 def decode_bytes(m: int, k: int, n: int, g: int = G) -> int:
@@ -89,57 +103,143 @@ def make_weights(k: int, n: int, copies: int, dev):
     return out
 
 
-def cpu_baseline(time_budget_s: float = 12.0) -> dict:
-    """The reference CPU path timed on this host over passes of the decode sweep."""
+def _median_time(fn, reps: int) -> float:
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_baseline() -> dict:
+    """The reference CPU path timed on this host: the reference test oracle
+    (pulsar/tests/test_w4a16_gemm.py:56-62), i.e. dequantize the whole weight
+    to fp32, then an fp32 GEMM, per call.  Dequant: oracle/w4a16_oracle.c
+    (OpenMP); GEMM: numpy's BLAS sgemm (oracle.gemm_f32_blas).  A call's time is
+    its dequant's plus its GEMM's, each timed on its own: every dequant is
+    timed before the first BLAS call, because BLAS worker threads keep spinning
+    for a while after a GEMM and would take the cores from the OpenMP dequant
+    (an artefact of two thread pools in one process, not part of the path).
+    Bounded samples of every BASELINE config:
+      value  - configs[1], the 16 decode-sweep GEMMs: bytes over the summed
+               per-call times (dequant and GEMM each a median of 5), GB/s;
+      config1_m1_k4096_n4096 - configs[0], its two phases apart (median of 5);
+      prefill - configs[2]: GEMM at M = 256 and 1024 (median of 3 / 1) and at
+                M = 4096 timed on 1024 rows and scaled by 4 (rows of a GEMM
+                cost alike), plus the layer's dequant;
+      act_order_70b - configs[3]: the asymmetric act-order dequant of each 70B
+                layer (once), GEMM at M = 1, 16 (median of 3) and at M = 2048
+                timed on 256 rows and scaled by 8;
+      stack  - configs[4]: one Llama-3-8B layer's seven linears at M = 1 and
+               32 (median of 3 each phase) times 32 layers (the layers have
+               the same shapes), per decode token."""
     import numpy as np
 
     from oracle import oracle as O
+    from pulsar_amd.stack import LLAMA3_8B_LINEARS
 
+    t_start = time.perf_counter()
     rng = np.random.default_rng(0)
-    data = []
-    for _, k, n in LLAMA8B:
-        packed = rng.integers(-(2 ** 31), 2 ** 31, size=(n, k // 8), dtype=np.int64).astype(np.int32)
-        scale = (np.abs(rng.standard_normal((n, k // G))) * 0.02 + 1e-3).astype(np.float32)
-        data.append((k, n, packed, scale, np.empty((n, k), dtype=np.float32)))
-    xs = {(m, k): rng.standard_normal((m, k)).astype(np.float32) for m in DECODE_M for _, k, _ in LLAMA8B}
-    tot_bytes, tot_time, gemms = 0, 0.0, 0
-    while tot_time < time_budget_s:
-        for m in DECODE_M:
-            for k, n, packed, scale, wbuf in data:
-                t0 = time.perf_counter()
-                O.w4a16_ct_forward(xs[(m, k)], packed, scale, G, wbuf)
-                tot_time += time.perf_counter() - t0
-                tot_bytes += decode_bytes(m, k, n)
-                gemms += 1
-    # BASELINE configs[0] (M = 1, K = N = 4096) on the same path, its two phases timed apart:
-    # median of 5 runs each
-    k1 = n1 = 4096
-    packed1 = rng.integers(-(2 ** 31), 2 ** 31, size=(n1, k1 // 8), dtype=np.int64).astype(np.int32)
-    scale1 = (np.abs(rng.standard_normal((n1, k1 // G))) * 0.02 + 1e-3).astype(np.float32)
-    x1 = rng.standard_normal((1, k1)).astype(np.float32)
-    phases = {"dequant": [], "gemm": [], "total": []}
-    w1 = np.empty((n1, k1), dtype=np.float32)
-    for _ in range(6):  # the first pass faults the buffer in; medians over the last 5
+
+    def ct_weight(k, n, seed):
+        u = O.uint4(seed, 2, (n, k))
+        return O.pack_ct((u.astype(np.int16) - 8).astype(np.int8)), O.abs_normal(seed, 3, (n, k // G))
+
+    # ---- phase 1: every dequant, before any BLAS call -------------------------------------
+    def dq_ct(packed, scale):
+        w = np.empty((packed.shape[0], packed.shape[1] * 8), dtype=np.float32)
+        O.dequant_ct(packed, scale, G, out=w)
+        return w, _median_time(lambda: O.dequant_ct(packed, scale, G, out=w), 5)
+
+    l8 = {}
+    for i, (name, k, n) in enumerate(LLAMA8B):
+        l8[name] = dq_ct(*ct_weight(k, n, 10 + i))
+    w1, dq1 = dq_ct(*ct_weight(4096, 4096, 20))
+    l70 = {}
+    for i, (name, k, n) in enumerate(LLAMA70B):
+        p = O.make_problem(1, n, k, G, seed=30 + i, symmetric=False, act_order=True)
+        qw, qz, s_kn, g_idx = p.qweight(), p.qzeros(), p.scale_kn, p.g_idx
+        del p
         t0 = time.perf_counter()
-        O.dequant_ct(packed1, scale1, G, out=w1)
-        t1 = time.perf_counter()
-        O.gemm_f32(x1, w1)
-        t2 = time.perf_counter()
-        O.w4a16_ct_forward(x1, packed1, scale1, G, w1)
-        t3 = time.perf_counter()
-        phases["dequant"].append(t1 - t0)
-        phases["gemm"].append(t2 - t1)
-        phases["total"].append(t3 - t2)
-    config1 = {f"{k}_ms": round(sorted(v[1:])[2] * 1e3, 3) for k, v in phases.items()}
-    config1["GB/s"] = round(decode_bytes(1, k1, n1) / (sorted(phases["total"][1:])[2]) / 1e9, 3)
+        w = O.dequant_gptq(qw, s_kn, qz, g_idx, G)
+        l70[name] = (w, time.perf_counter() - t0)
+        del qw, qz
+    layer = []
+    for j, (_, k, n) in enumerate(LLAMA3_8B_LINEARS):
+        w, dq = dq_ct(*ct_weight(k, n, 40 + j))
+        layer.append((k, n, w, dq))
+
+    # ---- phase 2: the GEMMs ---------------------------------------------------------------
+    def gemm_time(w, rows, reps):
+        xm = rng.standard_normal((rows, w.shape[1])).astype(np.float32)
+        O.gemm_f32_blas(xm, w)
+        return _median_time(lambda: O.gemm_f32_blas(xm, w), reps)
+
+    tot_bytes = tot_time = 0.0
+    decode = {}
+    for m in DECODE_M:
+        for name, k, n in LLAMA8B:
+            w, dq = l8[name]
+            t = dq + gemm_time(w, m, 5)
+            decode[f"{name}_m{m}"] = round(t * 1e3, 3)
+            tot_bytes += decode_bytes(m, k, n)
+            tot_time += t
+    gm1 = gemm_time(w1, 1, 5)
+    config1 = {"dequant_ms": round(dq1 * 1e3, 3), "gemm_ms": round(gm1 * 1e3, 3),
+               "total_ms": round((dq1 + gm1) * 1e3, 3),
+               "GB/s": round(decode_bytes(1, 4096, 4096) / (dq1 + gm1) / 1e9, 3)}
+    prefill = {}
+    for name, k, n in LLAMA8B:
+        w, dq = l8[name]
+        for m, rows, reps in ((256, 256, 3), (1024, 1024, 1), (4096, 1024, 1)):
+            gm = gemm_time(w, rows, reps) * (m // rows)
+            prefill[f"{name}_m{m}"] = {"dequant_ms": round(dq * 1e3, 2), "gemm_ms": round(gm * 1e3, 2),
+                                       "total_ms": round((dq + gm) * 1e3, 2),
+                                       "TFLOP/s": round(2.0 * m * n * k / (dq + gm) / 1e12, 4),
+                                       **({"gemm_rows_timed": rows} if rows != m else {})}
+    act = {}
+    for name, k, n in LLAMA70B:
+        w, dq = l70[name]
+        res = {"dequant_ms": round(dq * 1e3, 1)}
+        for m, rows, reps in ((1, 1, 3), (16, 16, 3), (2048, 256, 1)):
+            gm = gemm_time(w, rows, reps) * (m // rows)
+            r = {"gemm_ms": round(gm * 1e3, 2), "total_ms": round((dq + gm) * 1e3, 1)}
+            if m <= 16:
+                r["GB/s"] = round(act_order_bytes(m, k, n) / (dq + gm) / 1e9, 3)
+            else:
+                r["TFLOP/s"] = round(2.0 * m * n * k / (dq + gm) / 1e12, 4)
+                r["gemm_rows_timed"] = rows
+            res[f"m{m}"] = r
+        act[name] = res
+    del l70
+    stack = {}
+    for m in STACK_M:
+        t = sum(dq + gemm_time(w, m, 3) for _, _, w, dq in layer)
+        nbytes = STACK_LAYERS * sum(decode_bytes(m, k, n) for k, n, _, _ in layer)
+        stack[f"m{m}"] = {"layer_ms": round(t * 1e3, 2), "ms_per_token": round(t * STACK_LAYERS * 1e3, 1),
+                          "bytes_per_token": nbytes, "GB/s": round(nbytes / (t * STACK_LAYERS) / 1e9, 3)}
+
     return {
         "value": round(tot_bytes / tot_time / 1e9, 3),
         "unit": "GB/s",
         "cores": O.num_threads(),
+        "blas_threads": O.blas_threads(),
         "kind": "port",
-        "sample": f"{gemms // 16} passes over the 16 decode-sweep GEMMs ({gemms} GEMMs, {tot_time:.1f} s of CPU "
-                  "work): dequantize to fp32 + OpenMP fp32 GEMM, oracle/w4a16_oracle.c",
+        "sample": "value: the 16 decode-sweep GEMMs once each, a call = full dequantize to fp32 (oracle/"
+                  "w4a16_oracle.c, OpenMP) + fp32 BLAS GEMM, each phase a median of 5; prefill, act_order_70b "
+                  "and stack as in their notes",
+        "decode_ms": decode,
         "config1_m1_k4096_n4096": config1,
+        "prefill": prefill,
+        "act_order_70b": act,
+        "stack": stack,
+        "notes": {"prefill": "per layer: dequant median of 5; GEMM M=256 median of 3, M=1024 once, M=4096 timed "
+                             "on 1024 rows x 4",
+                  "act_order_70b": "asymmetric act-order dequant (zero points, g_idx) once per layer; GEMM M=1, 16 "
+                                   "median of 3, M=2048 timed on 256 rows x 8",
+                  "stack": "one layer's 7 linears (dequant median of 5, GEMM median of 3) x 32 layers"},
+        "cpu_seconds": round(time.perf_counter() - t_start, 1),
     }
 
 
@@ -254,6 +354,46 @@ def summarize_traffic(fetch_csv: str, write_csv: str) -> int:
     path = os.path.join(ROOT, "profiles", "decode_traffic.json")
     with open(path, "w") as f:
         json.dump(res, f, indent=1)
+    print(json.dumps(res))
+    return 0
+
+
+def summarize_trace(trace_csv: str, steps: int) -> int:
+    """Recompute `roofline` from a rocprofv3 --kernel-trace CSV of this bench.
+
+    The roofline leg runs last among the decode launches: per shape, in the sweep
+    order, steps*REPS unarmed calls, then as many armed ones.  So the trace's last
+    16 * 2 * steps * REPS decode_kernel dispatches are that leg; their mean
+    duration per shape, and the algorithmic bytes over the mean of those means,
+    give the figure the bench computes from its own events."""
+    import csv
+
+    rows = [r for r in csv.DictReader(open(trace_csv)) if "decode_kernel" in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    reps = steps * REPS
+    shapes = [(m, name, k, n) for m in DECODE_M for name, k, n in LLAMA8B]
+    need = len(shapes) * 2 * reps
+    if len(rows) < need:
+        print(f"{trace_csv}: {len(rows)} decode dispatches, the roofline leg needs {need}", file=sys.stderr)
+        return 1
+    leg = rows[-need:]
+    per_shape, unarmed_all, armed_all = {}, [], []
+    for i, (m, name, k, n) in enumerate(shapes):
+        d = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in leg[i * 2 * reps:(i + 1) * 2 * reps]]
+        un, ar = d[:reps], d[reps:]
+        per_shape[f"{name}_m{m}"] = {"unarmed_us": round(sum(un) / reps, 3), "armed_us": round(sum(ar) / reps, 3)}
+        unarmed_all.append(sum(un) / reps)
+        armed_all.append(sum(ar) / reps)
+    alg = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) / len(shapes)
+    res = {"decode_dispatches_in_trace": len(rows), "roofline_leg_dispatches": need,
+           "mean_unarmed_us": round(sum(unarmed_all) / len(shapes), 3),
+           "mean_armed_us": round(sum(armed_all) / len(shapes), 3),
+           "algorithmic_bytes_per_launch": round(alg)}
+    for tag in ("unarmed", "armed"):
+        us = res[f"mean_{tag}_us"]
+        res[f"achieved_{tag}_GB/s"] = round(alg / (us * 1e-6) / 1e9, 1)
+        res[f"frac_{tag}"] = round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    res["per_shape"] = per_shape
     print(json.dumps(res))
     return 0
 
@@ -389,8 +529,109 @@ def act_order_bench(torch, dev, steps: int, warmup: int) -> dict:
     return out
 
 
+READ_BYTES = 1 << 30
+
+
+def measure_read_ceiling(torch, dev) -> dict:
+    """HBM read-only rate over 1 GiB (four times the MALL): the streaming-read probe
+    (pulsar_amd/libpw4_probe.so, 16-byte loads, grid-stride) at a few grid sizes, median of
+    5 each, the best reported; torch reductions over the same buffer alongside."""
+    import ctypes
+
+    import pulsar_amd
+
+    t = torch.ones(READ_BYTES // 4, dtype=torch.int32, device=dev)
+    sink = torch.zeros(1024, dtype=torch.int32, device=dev)
+
+    def rate(fn):
+        fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
+        for a, b in ev:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        ms = sorted(a.elapsed_time(b) for a, b in ev)[2]
+        return round(READ_BYTES / (ms * 1e-3) / 1e9, 1)
+
+    probe = ctypes.CDLL(os.path.join(os.path.dirname(pulsar_amd.__file__), "libpw4_probe.so"))
+    probe.pw4_probe_stream_read.restype = ctypes.c_int
+    probe.pw4_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32,
+                                            ctypes.c_void_p, ctypes.c_void_p]
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def read(blocks):
+        rc = probe.pw4_probe_stream_read(t.data_ptr(), READ_BYTES, blocks, 0xDEADBEEF, sink.data_ptr(), stream)
+        if rc != 0:
+            raise RuntimeError(f"pw4_probe_stream_read failed: hipError {rc}")
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    probe_rates = {f"probe_{w}x{cus}_wg": rate(lambda w=w: read(w * cus)) for w in (1, 2, 4, 8, 16)}
+    torch_rates = {"torch_amax_int32": rate(lambda: t.amax()), "torch_sum_f32": rate(lambda: t.view(torch.float32).sum())}
+    del t, sink
+    best = max(probe_rates, key=probe_rates.get)
+    return {"GB/s": probe_rates[best], "op": best, "all": {**probe_rates, **torch_rates}, "bytes_read": READ_BYTES,
+            "what": "streaming read of 1 GiB (16-byte loads, grid-stride, workgroups of 256), median of 5, bytes "
+                    "read; the best grid of the probe"}
+
+
+def repack_bench(torch, dev) -> dict:
+    """repack_w4a16 (the reference's one-time CT -> MARLIN repack) per Llama-3-8B layer:
+    HIP events around each call on two copies in turn, median of 5.  Bytes: the CT words
+    read and the MARLIN words written, plus the scales read (fp16) and written (fp32)."""
+    import pulsar_amd
+
+    out = {}
+    for name, k, n in LLAMA8B:
+        srcs = []
+        for _ in range(2):
+            packed = torch.randint(-(2 ** 31), 2 ** 31, (n, k // 8), dtype=torch.int32, device=dev)
+            scale = (torch.randn(n, k // G, device=dev) * 0.02).abs_().add_(1e-3).half()
+            srcs.append((packed, scale))
+        pulsar_amd.ops.repack_w4a16(*srcs[0], G)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
+        for i, (a, b) in enumerate(ev):
+            a.record()
+            pulsar_amd.ops.repack_w4a16(*srcs[i % 2], G)
+            b.record()
+        torch.cuda.synchronize()
+        ms = sorted(a.elapsed_time(b) for a, b in ev)[2]
+        nbytes = n * k // 2 * 2 + n * (k // G) * (2 + 4)
+        out[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+        del srcs
+    return out
+
+
+def dense_yardstick(torch, dev, reps: int) -> dict:
+    """What the dense fp16 library GEMM (torch.nn.functional.linear -> hipBLASLt) does at
+    the M = 4096 prefill shapes with the same kind of data (x ~ N(0,1), weights ~ N(0,1)*0.02
+    in fp16): a measured ceiling for the W4A16 prefill next to the nameplate peak."""
+    out = {}
+    m = PREFILL_M[-1]
+    for name, k, n in LLAMA8B:
+        x = torch.randn(m, k, device=dev).half()
+        w = (torch.randn(n, k, device=dev) * 0.02).half()
+        for _ in range(2):
+            torch.nn.functional.linear(x, w)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in ev:
+            a.record()
+            torch.nn.functional.linear(x, w)
+            b.record()
+        torch.cuda.synchronize()
+        ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        out[f"{name}_m{m}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+                               "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3)}
+        del x, w
+    return out
+
+
 def time_each_launch(torch, shapes, weights, xs, fn, stream, reps: int) -> tuple[list[float], list[float]]:
-    """Per shape, the mean duration (ms) of single decode-kernel launches, two ways:
+    """Per shape, the mean duration (ms) of single decode-kernel launches, each on the
+    next of the layer's weight copies (>= 512 MB of them, so every launch streams its
+    weights from HBM, not from the 256 MB MALL), two ways:
     * the kernel's own: each call arms pw4_time_next_kernel with a pair of HIP events,
       which the library passes to hipExtLaunchKernel; they take the dispatch's start and
       end timestamps, the interval rocprofv3's kernel trace reports;
@@ -410,14 +651,15 @@ def time_each_launch(torch, shapes, weights, xs, fn, stream, reps: int) -> tuple
             for a, b in kev:  # create the events before handing them over
                 a.record(stream)
                 b.record(stream)
+            ncp = len(weights[name])
             for r in range(reps):  # unarmed calls: a hooked launch costs the runtime more
                 cev[r][0].record(stream)
-                fn(xs[(m, k)], weights[name][(first + r) % COPIES])
+                fn(xs[(m, k)], weights[name][(first + r) % ncp])
                 cev[r][1].record(stream)
             for r in range(reps):
                 if lib.pw4_time_next_kernel(kev[r][0], kev[r][1]) != 0:
                     raise RuntimeError("pw4_time_next_kernel failed")
-                fn(xs[(m, k)], weights[name][(first + r) % COPIES])
+                fn(xs[(m, k)], weights[name][(first + r) % ncp])
             stream.synchronize()
             ko = [a.elapsed_time(b) for a, b in kev]
             call.append(sum(a.elapsed_time(b) for a, b in cev) / reps)
@@ -444,9 +686,14 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true", help="skip the decode sweep (headline value null)")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise the two --pmc-workload counter CSVs into profiles/decode_traffic.json")
+    ap.add_argument("--trace", metavar="KERNEL_TRACE_CSV",
+                    help="recompute the roofline from a rocprofv3 --kernel-trace CSV of this bench run with "
+                         "the same --steps")
     args = ap.parse_args()
     if args.traffic:
         return summarize_traffic(*args.traffic)
+    if args.trace:
+        return summarize_trace(args.trace, args.steps)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the W4A16 path has no multi-GPU component in this build "
               "(--gpus must be 1)", file=sys.stderr)
@@ -458,7 +705,8 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
-    weights = {name: make_weights(k, n, COPIES, dev) for name, k, n in LLAMA8B}
+    weights = {name: make_weights(k, n, copies_for(k, n), dev) for name, k, n in LLAMA8B}
+    copy_counts = {name: len(w) for name, w in weights.items()}
     xs = {(m, k): torch.randn(m, k, device=dev).half() for m in DECODE_M for _, k, _ in LLAMA8B}
     shapes = [(m, name, k, n) for m in DECODE_M for name, k, n in LLAMA8B]
     stream = torch.cuda.Stream(device=dev)
@@ -479,7 +727,7 @@ def main() -> int:
         with torch.cuda.stream(stream):
             for m, name, k, n in shapes:
                 for r in range(REPS):
-                    gemm_fp16_scales(xs[(m, k)], weights[name][r % COPIES])
+                    gemm_fp16_scales(xs[(m, k)], weights[name][r % len(weights[name])])
             src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device=dev)
             dst = torch.empty_like(src)
             dst.copy_(src)
@@ -523,9 +771,12 @@ def main() -> int:
                    "per_gemm_us": {f"{name}_m{m}": round(ms * 1e3, 2) for (m, name, _, _), ms in zip(shapes, per2)}}
         del g2
 
-    # achievable-HBM context: a 512 MiB device-to-device copy (read + write bytes)
-    copy_ceiling = None
+    # achievable-HBM context: a 512 MiB device-to-device copy (read + write bytes), and
+    # read-only streams of 1 GiB (torch reductions: the weights of a decode GEMM are read,
+    # never written)
+    copy_ceiling = read_ceiling = None
     if not args.no_decode:
+        read_ceiling = measure_read_ceiling(torch, dev)
         src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device=dev)
         dst = torch.empty_like(src)
         dst.copy_(src)
@@ -560,7 +811,7 @@ def main() -> int:
                 ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                       for _ in range(args.prefill_reps)]
                 for i, (a, b) in enumerate(ev):
-                    w = weights[name][i % COPIES]
+                    w = weights[name][i % len(weights[name])]
                     a.record()
                     gemm_fp16_scales(x, w)
                     b.record()
@@ -570,6 +821,8 @@ def main() -> int:
                 prefill[f"{name}_m{pm}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
                                             "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3)}
                 del x
+    repack = None if args.no_prefill else repack_bench(torch, dev)
+    dense = None if args.no_prefill else dense_yardstick(torch, dev, args.prefill_reps)
     del weights, xs
     torch.cuda.empty_cache()
 
@@ -602,9 +855,10 @@ def main() -> int:
                         "gate_up 4096x28672, down 14336x4096}, symmetric int4 G=128 fp16 scales, MARLIN "
                         "layout, fp16 x",
             "launches_per_gemm_per_step": REPS,
-            "weight_copies": COPIES,
-            "mall_safe": f"each layer rotates over {COPIES} weight copies; a copy is reused after ~850 MB "
-                         "of other weights",
+            "weight_copies": copy_counts,
+            "mall_safe": "each layer rotates over copies holding >= 512 MB (the MALL is 256 MB): in the "
+                         "graphs a copy is reused after ~850 MB of other weights, and the roofline's single "
+                         "launches walk each layer's copies in turn",
             "timing": "per-shape HIP graphs of back-to-back launches, HIP events on the replay stream",
         },
         "roofline": {
@@ -624,10 +878,15 @@ def main() -> int:
                 "(the kernel timing events did not fire on this box; queue latency included)"),
             "mean_call_us": None if mean_call_us is None else round(mean_call_us, 3),
             "copy_ceiling": copy_ceiling,
+            "read_ceiling": read_ceiling,
+            "frac_of_read_ceiling": None if achieved is None or read_ceiling is None else
+            round(achieved / read_ceiling["GB/s"], 4),
         },
         "decode": per_gemm,
         "reference_api": ref_api,
         "prefill": prefill,
+        "prefill_dense_fp16_yardstick": dense,
+        "repack": repack,
         "stack": stack,
         "act_order_70b": act_order,
         "cpu_baseline": cpu,

@@ -306,6 +306,29 @@ def gemm_f32(x: np.ndarray, w: np.ndarray) -> np.ndarray:
     return out
 
 
+def gemm_f32_blas(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """The same y[M,N] = x[M,K] @ w[N,K]^T in fp32 through numpy's BLAS sgemm:
+    the reference oracle's `x.float() @ w_deq.t()` (pulsar/tests/
+    test_w4a16_gemm.py:56-62) as a CPU library runs it.  Used for the timed CPU
+    baseline, where the C loop nest above would understate the CPU; pinned
+    against gemm_f32 and a float64 matmul."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    assert x.shape[1] == w.shape[1]
+    return np.matmul(x, w.T)
+
+
+def blas_threads() -> int | None:
+    """Threads of the BLAS behind gemm_f32_blas (None when it cannot tell)."""
+    try:
+        from threadpoolctl import threadpool_info
+
+        n = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
+        return int(max(n)) if n else None
+    except Exception:  # noqa: BLE001 -- informational only
+        return None
+
+
 def gemm_f32_split(x: np.ndarray, w: np.ndarray, splits: int) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     w = np.ascontiguousarray(w, dtype=np.float32)

@@ -4,7 +4,12 @@
 
 produces, next to this file,
   libpulsar_w4a16.so          HIP kernels + the C ABI of include/pulsar_w4a16.h
-  _pulsar_w4a16_torch.so      at::Tensor API + torch.ops.pulsar registration
+  _pulsar_w4a16_torch.so      at::Tensor API + torch.ops.pulsar registration, and the
+                              C++ model layer of include/pulsar_w4a16_model.hpp
+                              (torch.classes.pulsar.Qwen3W4A16Layer)
+  libpw4_probe.so             a streaming-read probe that bench.py times for the
+                              read-only HBM ceiling (measurement only; not part of
+                              the library or its ABI)
 """
 
 from __future__ import annotations
@@ -25,6 +30,9 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIP_SOURCES = ["repack.hip", "gemm_decode.hip", "gemm_prefill.hip", "gemm_prefill_256.hip", "capi.hip"]
 LIB_NAME = "libpulsar_w4a16.so"
 TORCH_LIB_NAME = "_pulsar_w4a16_torch.so"
+TORCH_SOURCES = ["torch_ops.cpp", "model.cpp"]
+PROBE_SOURCE = "probe.hip"
+PROBE_LIB_NAME = "libpw4_probe.so"
 
 # gfx950 only.  Packed-fp32 instructions are disabled for the device pass; the
 # host pass prints a harmless "not a recognized feature" warning for it.
@@ -109,7 +117,7 @@ def build_torch(verbose: bool = False) -> str:
         os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared",
         f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
         *inc, f"-I{py_inc}", f"-I{ROCM}/include", f"-I{INCLUDE}",
-        os.path.join(CSRC, "torch_ops.cpp"), "-o", tmp,
+        *[os.path.join(CSRC, f) for f in TORCH_SOURCES], "-o", tmp,
         f"-L{HERE}", "-lpulsar_w4a16", f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
         "-ltorch_hip", f"-L{ROCM}/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}",
     ]
@@ -118,9 +126,18 @@ def build_torch(verbose: bool = False) -> str:
     return out
 
 
+def build_probe(verbose: bool = False) -> str:
+    out = os.path.join(HERE, PROBE_LIB_NAME)
+    tmp = out + ".tmp"
+    _run_parallel([[_hipcc(), *HIPCC_FLAGS, "-shared", os.path.join(CSRC, PROBE_SOURCE), "-o", tmp]], verbose)
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False) -> None:
     build_hip(verbose)
     build_torch(verbose)
+    build_probe(verbose)
 
 
 if __name__ == "__main__":

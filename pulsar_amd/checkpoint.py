@@ -116,21 +116,58 @@ def _read_config(source: str) -> dict:
             return {}
 
 
+def _shard_files(source: str) -> list[str]:
+    roots = [source, os.path.join(source, "weights")]
+    return sorted({os.path.join(r, f) for r in roots if os.path.isdir(r) for f in os.listdir(r)
+                   if f.endswith(".safetensors")})
+
+
+def _zip_members(z: zipfile.ZipFile) -> list[str]:
+    return sorted(n for n in z.namelist() if n.startswith("weights/") and n.endswith(".safetensors"))
+
+
+def _header_names(f) -> list[str]:
+    """Tensor names from a safetensors header (8-byte little-endian length, then JSON),
+    without reading the tensor data."""
+    n = int.from_bytes(f.read(8), "little")
+    return [k for k in json.loads(f.read(n)) if k != "__metadata__"]
+
+
+def _tensor_names(source: str) -> list[str]:
+    """Every tensor name of `source` (directory or zip archive), from the shard headers only."""
+    names = []
+    if os.path.isdir(source):
+        for path in _shard_files(source):
+            with open(path, "rb") as f:
+                names += _header_names(f)
+        return names
+    with zipfile.ZipFile(source) as z:
+        for member in _zip_members(z):
+            with z.open(member) as f:
+                names += _header_names(f)
+    return names
+
+
 def _iter_shards(source: str):
-    """(name, cpu tensor) over every safetensors shard of `source` (directory or zip archive)."""
+    """(name, cpu tensor) over every safetensors shard of `source` (directory or zip archive),
+    one tensor at a time: a directory's shards are memory-mapped, a zip member is read whole
+    (one shard in host memory at a time)."""
+    from safetensors import safe_open
     from safetensors.torch import load as st_load
-    from safetensors.torch import load_file
 
     if os.path.isdir(source):
-        roots = [source, os.path.join(source, "weights")]
-        files = sorted({os.path.join(r, f) for r in roots if os.path.isdir(r) for f in os.listdir(r)
-                        if f.endswith(".safetensors")})
-        for path in files:
-            yield from load_file(path).items()
+        for path in _shard_files(source):
+            with safe_open(path, framework="pt", device="cpu") as f:
+                for name in f.keys():
+                    yield name, f.get_tensor(name)
         return
     with zipfile.ZipFile(source) as z:
-        for member in sorted(n for n in z.namelist() if n.startswith("weights/") and n.endswith(".safetensors")):
-            yield from st_load(z.read(member)).items()
+        for member in _zip_members(z):
+            shard = st_load(z.read(member))
+            while shard:
+                name = next(iter(shard))
+                yield name, shard.pop(name)
+            del shard
 
 
 # ---- the loader ----------------------------------------------------------------------------
@@ -190,8 +227,7 @@ def load_weights(source: str, *, device: torch.device | str, dtype: torch.dtype 
     device = torch.device(device)
     cfg = _read_config(source)
     qraw = quant if quant is not None else cfg.get("quantization_config")
-    tensors = dict(_iter_shards(source))
-    prefixes = find_quantized(tensors)
+    prefixes = find_quantized(_tensor_names(source))  # from the shard headers, before any data
     if prefixes and qraw is None:
         raise CheckpointError("quantized linears found but no quantization_config (pass quant=...)")
     qc = parse_quant_config(qraw) if prefixes else None
@@ -200,19 +236,20 @@ def load_weights(source: str, *, device: torch.device | str, dtype: torch.dtype 
                               f"{sorted(set(prefixes.values()))} linears")
     out: dict = {}
     groups: dict[str, dict[str, torch.Tensor]] = {p: {} for p in prefixes}
-    for name, t in tensors.items():
+    # each tensor goes to the device as it is read, so host memory holds one shard at most
+    for name, t in _iter_shards(source):
         if _is_member(name, prefixes):
             p, _, suffix = name.rpartition(".")
             groups[p][suffix] = t.to(device)
         else:
             out[name] = t.to(device=device, dtype=dtype if (dtype is not None and t.is_floating_point()) else None)
+        del t
     for p, fmt in prefixes.items():
         lin = build_linear(fmt, groups.pop(p), qc, p)
         bias = out.pop(p + ".bias", None)
         if bias is not None:
             lin.bias = bias.to(torch.float32)
         out[p + ".weight"] = lin
-    del tensors
     if fuse:
         fuse_projections(out, silu_gate=silu_gate)
     return out
@@ -221,19 +258,26 @@ def load_weights(source: str, *, device: torch.device | str, dtype: torch.dtype 
 def fuse_projections(weights: dict, silu_gate: bool = False) -> None:
     """In place: `<l>.self_attn.{q,k,v}_proj.weight` -> `<l>.self_attn.qkv_proj.weight` and
     `<l>.mlp.{gate,up}_proj.weight` -> `<l>.mlp.gate_up_proj.weight` (a W4A16SiluGate with
-    `silu_gate`), for every layer whose members are all W4A16Linear (Llama / Qwen naming)."""
+    `silu_gate`), for every layer whose members are all W4A16Linear (Llama / Qwen naming) and
+    can share one GEMM.  Members that cannot (different act-order permutations, as desc_act
+    checkpoints usually have, or zero points kept on some and dropped as all-8 on others) stay
+    separate linears under their own names."""
     for key in [k for k in weights if k.endswith(".self_attn.q_proj.weight")]:
         base = key[: -len("q_proj.weight")]
         names = [base + m + "_proj.weight" for m in ("q", "k", "v")]
-        if all(isinstance(weights.get(n), W4A16Linear) for n in names):
+        if all(isinstance(weights.get(n), W4A16Linear) for n in names) and \
+                W4A16Linear.can_concat([weights[n] for n in names]):
             weights[base + "qkv_proj.weight"] = W4A16Linear.concat([weights.pop(n) for n in names])
     for key in [k for k in weights if k.endswith(".mlp.gate_proj.weight")]:
         base = key[: -len("gate_proj.weight")]
         names = [base + m + "_proj.weight" for m in ("gate", "up")]
-        if all(isinstance(weights.get(n), W4A16Linear) for n in names):
-            members = [weights.pop(n) for n in names]
-            weights[base + "gate_up_proj.weight"] = (W4A16SiluGate.from_members(*members) if silu_gate
-                                                     else W4A16Linear.concat(members))
+        if not all(isinstance(weights.get(n), W4A16Linear) for n in names):
+            continue
+        members = [weights[n] for n in names]
+        if silu_gate and W4A16SiluGate.can_fuse(*members):
+            weights[base + "gate_up_proj.weight"] = W4A16SiluGate.from_members(*[weights.pop(n) for n in names])
+        elif not silu_gate and W4A16Linear.can_concat(members):
+            weights[base + "gate_up_proj.weight"] = W4A16Linear.concat([weights.pop(n) for n in names])
 
 
 def save_archive(path: str, config: dict, tensors: dict[str, torch.Tensor], shards: int = 1) -> None:

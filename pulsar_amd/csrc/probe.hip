@@ -1,0 +1,49 @@
+// Measurement probe for bench.py (libpw4_probe.so, not part of the W4A16
+// library or its C ABI): a plain streaming read of a device buffer, the
+// read-only HBM rate a memory-bound kernel can expect on this device.
+//
+// Each thread reads 16-byte vectors in a grid-stride loop, four loads in
+// flight per iteration, and folds them into an XOR; the fold is stored only if
+// it equals a value the caller never passes (`sink` is written by no launch in
+// practice), so the loads stay but nothing is written.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ p, int64_t n16,
+                                                          uint32_t never, uint32_t* __restrict__ sink) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const u32x4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
+        acc ^= a ^ b ^ c ^ d;
+    }
+    for (; i < n16; i += stride) acc ^= p[i];
+    const uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+    if (v == never) sink[blockIdx.x & 1023] = v;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Reads `bytes` (a multiple of 16) from the 16-byte aligned device buffer `p` with
+// `blocks` workgroups of 256 threads on `stream`.  `sink` is a device buffer of at
+// least 1024 uint32 that the kernel writes only if the XOR of everything it read
+// equals `never`.  Returns a hipError_t.
+int pw4_probe_stream_read(const void* p, int64_t bytes, int blocks, uint32_t never, uint32_t* sink,
+                          hipStream_t stream) {
+    if (p == nullptr || sink == nullptr || bytes <= 0 || bytes % 16 != 0 || blocks <= 0 ||
+        (reinterpret_cast<uintptr_t>(p) & 15) != 0) {
+        return (int)hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       reinterpret_cast<const u32x4*>(p), bytes / 16, never, sink);
+    return (int)hipGetLastError();
+}
+
+}  // extern "C"

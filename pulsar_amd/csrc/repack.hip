@@ -10,9 +10,12 @@
 // word tg = sum_j (b_j & 0xf) << 4j | (b_j >> 4) << (16 + 4j).
 //
 // The reference builds each word with eight scattered nibble reads
-// (w4a16_marlin.cu:139-174); here each thread reads the tile's four source
-// words once and writes 16 contiguous bytes, so for a fixed tile the threads
-// of a 64-column block write one contiguous 1 KB run.
+// (w4a16_marlin.cu:139-174); here a thread turns one (n, t) tile's four source
+// words into its 16 output bytes in registers.  A workgroup takes a 64-column
+// block and 16 tiles (512 K): for the CT layout its lanes read each source row
+// as 256-byte runs, the transformed tiles pass through LDS, and each tile of
+// the block leaves as one contiguous 1 KB run; GPTQ rows are [K/8, N], so
+// lanes over n read them coalesced as they are and no LDS is needed.
 #include "w4a16_common.h"
 #include "w4a16_kernels.h"
 
@@ -39,53 +42,93 @@ __device__ __forceinline__ int64_t marlin_offset(int n, int t, int nchunks) {
     return ((int64_t)(n >> 6) * nchunks + (t >> 1)) * kChunkWords + (t & 1) * 256 + (n & 63) * 4;
 }
 
-// compressed-tensors [N, K/8] (signed) -> MARLIN.  grid: (Npad/64, Kpad/32), block 64.
-__global__ __launch_bounds__(64) void repack_ct_kernel(const uint32_t* __restrict__ packed, uint32_t* __restrict__ wm,
-                                                       int N, int K, int nchunks) {
-    const int n = blockIdx.x * 64 + threadIdx.x;
-    const int t = blockIdx.y;
-    uint32_t src[4];
+constexpr int kRepackThreads = 256;
+constexpr int kRepackTiles = 16;  // 32-K tiles per workgroup (a multiple of 2: whole MARLIN chunks)
+
+// compressed-tensors [N, K/8] (signed) -> MARLIN.  grid: (Npad/64, Kpad/512 rounded up).
+// Read: item r = (row r / 16, tile r % 16) of the block, 16 lanes per 256-byte run of a
+// row.  Write: item r = (tile r / 64, column r % 64), 64 lanes per 1 KB run.  LDS rows are
+// padded by 16 bytes so the column-wise reads of the write phase spread over the banks.
+// VEC: rows are 16-byte aligned (K % 32 == 0, aligned base), so a whole tile of a row
+// is one 16-byte load; otherwise every tile is read word by word.
+template <bool VEC>
+__global__ __launch_bounds__(kRepackThreads) void repack_ct_kernel(const uint32_t* __restrict__ packed,
+                                                                   uint32_t* __restrict__ wm, int N, int K,
+                                                                   int nchunks) {
+    constexpr int kRow = kRepackTiles + 1;  // u32x4 per LDS row
+    __shared__ u32x4 tiles[64 * kRow];
+    const int n0 = blockIdx.x * 64, t0 = blockIdx.y * kRepackTiles;
+    const int ktiles = nchunks * 2;  // tiles in the padded layout
+    const int64_t rw = K / 8;        // source words per row
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int k = t * 32 + j * 8;  // K % 8 == 0: a source word is all-in or all-out
-        // signed nibble s -> u = s ^ 8; out-of-range -> u = 8 (dequantizes to 0)
-        src[j] = (n < N && k < K) ? (packed[(int64_t)n * (K / 8) + k / 8] ^ 0x88888888u) : 0x88888888u;
+    for (int q = 0; q < 64 * kRepackTiles / kRepackThreads; ++q) {
+        const int r = q * kRepackThreads + threadIdx.x;
+        const int row = r / kRepackTiles, tt = r % kRepackTiles;
+        const int n = n0 + row, t = t0 + tt;
+        uint32_t src[4];
+        if (VEC && n < N && t * 32 + 32 <= K) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(packed + (int64_t)n * rw + t * 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) src[j] = v[j] ^ 0x88888888u;  // signed s -> u = s ^ 8
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = t * 32 + j * 8;  // K % 8 == 0: a source word is all-in or all-out
+                src[j] = (n < N && k < K) ? (packed[(int64_t)n * rw + k / 8] ^ 0x88888888u) : 0x88888888u;
+            }
+        }
+        tiles[row * kRow + tt] = transpose_tile_bytes(src);
     }
-    *reinterpret_cast<u32x4*>(wm + marlin_offset(n, t, nchunks)) = transpose_tile_bytes(src);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 64 * kRepackTiles / kRepackThreads; ++q) {
+        const int r = q * kRepackThreads + threadIdx.x;
+        const int tt = r / 64, col = r % 64;
+        const int t = t0 + tt;
+        if (t < ktiles) *reinterpret_cast<u32x4*>(wm + marlin_offset(n0 + col, t, nchunks)) = tiles[col * kRow + tt];
+    }
 }
 
 // GPTQ qweight [K/8, N] (unsigned) -> MARLIN, rows gathered through perm when
-// given (repacked row j = original row perm[j]).  grid: (Npad/64, Kpad/32).
-__global__ __launch_bounds__(64) void repack_gptq_kernel(const uint32_t* __restrict__ qweight,
-                                                         const int32_t* __restrict__ perm,
-                                                         uint32_t* __restrict__ wm, int N, int K, int nchunks) {
-    const int n = blockIdx.x * 64 + threadIdx.x;
-    const int t = blockIdx.y;
-    uint32_t src[4];
-    if (perm == nullptr) {
+// given (repacked row j = original row perm[j]).  grid: (Npad/64, Kpad/512 rounded
+// up); thread (column i % 64, tile i / 64 + 4q) for q < 4: for each source row the
+// 64 lanes of a wave read 256 contiguous bytes and write one 1 KB output run.
+__global__ __launch_bounds__(kRepackThreads) void repack_gptq_kernel(const uint32_t* __restrict__ qweight,
+                                                                     const int32_t* __restrict__ perm,
+                                                                     uint32_t* __restrict__ wm, int N, int K,
+                                                                     int nchunks) {
+    const int n = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int ktiles = nchunks * 2;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int k = t * 32 + j * 8;
-            src[j] = (n < N && k < K) ? qweight[(int64_t)(k / 8) * N + n] : 0x88888888u;
-        }
-    } else {
+    for (int q = 0; q < kRepackTiles / 4; ++q) {
+        const int t = blockIdx.y * kRepackTiles + q * 4 + (threadIdx.x >> 6);
+        if (t >= ktiles) break;
+        uint32_t src[4];
+        if (perm == nullptr) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint32_t w = 0;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int k = t * 32 + j * 8 + e;
-                uint32_t nib = 8u;
-                if (n < N && k < K) {
-                    const int sk = min(max(perm[k], 0), K - 1);  // clamped: a bad perm cannot fault
-                    nib = (qweight[(int64_t)(sk >> 3) * N + n] >> (4 * (sk & 7))) & 0xfu;
-                }
-                w |= nib << (4 * e);
+            for (int j = 0; j < 4; ++j) {
+                const int k = t * 32 + j * 8;
+                src[j] = (n < N && k < K) ? qweight[(int64_t)(k / 8) * N + n] : 0x88888888u;
             }
-            src[j] = w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int k = t * 32 + j * 8 + e;
+                    uint32_t nib = 8u;
+                    if (n < N && k < K) {
+                        const int sk = min(max(perm[k], 0), K - 1);  // clamped: a bad perm cannot fault
+                        nib = (qweight[(int64_t)(sk >> 3) * N + n] >> (4 * (sk & 7))) & 0xfu;
+                    }
+                    w |= nib << (4 * e);
+                }
+                src[j] = w;
+            }
         }
+        *reinterpret_cast<u32x4*>(wm + marlin_offset(n, t, nchunks)) = transpose_tile_bytes(src);
     }
-    *reinterpret_cast<u32x4*>(wm + marlin_offset(n, t, nchunks)) = transpose_tile_bytes(src);
 }
 
 // scale_marlin[g, n] = (float) weight_scale[n, g]   (w4a16_marlin.cu:177-185)
@@ -144,8 +187,15 @@ __global__ __launch_bounds__(256) void gidx_perm_kernel(const int32_t* __restric
 hipError_t launch_repack_ct(const uint32_t* packed, uint32_t* wm, int N, int K, hipStream_t stream) {
     const int npad = (int)round_up(N, kMarlinBN), kpad = (int)round_up(K, kMarlinBK);
     if (npad == 0 || kpad == 0) return hipSuccess;
-    hipLaunchKernelGGL(repack_ct_kernel, dim3(npad / 64, kpad / 32), dim3(64), 0, stream, packed, wm, N, K,
-                       kpad / kMarlinBK);
+    // the 16-byte row reads need 16-byte aligned rows: K % 32 == 0 and an aligned base
+    const dim3 grid(npad / 64, (unsigned)ceil_div(kpad / 32, kRepackTiles));
+    if ((K % 32) != 0 || (reinterpret_cast<uintptr_t>(packed) & 15) != 0) {
+        hipLaunchKernelGGL(repack_ct_kernel<false>, grid, dim3(kRepackThreads), 0, stream, packed, wm, N, K,
+                           kpad / kMarlinBK);
+    } else {
+        hipLaunchKernelGGL(repack_ct_kernel<true>, grid, dim3(kRepackThreads), 0, stream, packed, wm, N, K,
+                           kpad / kMarlinBK);
+    }
     return hipGetLastError();
 }
 
@@ -153,8 +203,8 @@ hipError_t launch_repack_gptq(const uint32_t* qweight, const int32_t* perm, uint
                               hipStream_t stream) {
     const int npad = (int)round_up(N, kMarlinBN), kpad = (int)round_up(K, kMarlinBK);
     if (npad == 0 || kpad == 0) return hipSuccess;
-    hipLaunchKernelGGL(repack_gptq_kernel, dim3(npad / 64, kpad / 32), dim3(64), 0, stream, qweight, perm, wm, N, K,
-                       kpad / kMarlinBK);
+    hipLaunchKernelGGL(repack_gptq_kernel, dim3(npad / 64, (unsigned)ceil_div(kpad / 32, kRepackTiles)),
+                       dim3(kRepackThreads), 0, stream, qweight, perm, wm, N, K, kpad / kMarlinBK);
     return hipGetLastError();
 }
 

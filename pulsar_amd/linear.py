@@ -114,6 +114,25 @@ class W4A16Linear(torch.nn.Module):
     # ---- fusion ---------------------------------------------------------------------------
 
     @staticmethod
+    def can_concat(parts: list["W4A16Linear"]) -> bool:
+        """Whether `concat` accepts these members (see there)."""
+        if not parts:
+            return False
+        p0 = parts[0]
+        for i, p in enumerate(parts):
+            if isinstance(p, W4A16SiluGate):
+                return False
+            if (p.in_features, p.group_size, p.scales.dtype) != (p0.in_features, p0.group_size, p0.scales.dtype):
+                return False
+            if (p.qzeros is None) != (p0.qzeros is None) or (p.bias is None) != (p0.bias is None):
+                return False
+            if (p.perm is None) != (p0.perm is None) or (p.perm is not None and not torch.equal(p.perm, p0.perm)):
+                return False
+            if i + 1 < len(parts) and p.out_features % 64:
+                return False
+        return True
+
+    @staticmethod
     def concat(parts: list["W4A16Linear"]) -> "W4A16Linear":
         """N-concatenation of linears that share their input (q|k|v, gate|up).  Every member but
         the last needs N % 64 == 0 (no MARLIN padding inside the fused words); all need the same
@@ -165,6 +184,12 @@ class W4A16SiluGate(W4A16Linear):
     are gate 8j..8j+7, 16j+8..16j+15 are up 8j..8j+7), so every 16-column strip the kernels
     finish together carries matching gate and up columns; the reference runs two at::linear
     calls and at::silu(gate) * up (pulsar-core/src/model/qwen3.cpp:116-118)."""
+
+    @staticmethod
+    def can_fuse(gate: W4A16Linear, up: W4A16Linear) -> bool:
+        """Whether `from_members` accepts these two linears (see there)."""
+        return (W4A16Linear.can_concat([gate, up]) and gate.out_features == up.out_features and
+                gate.out_features % 64 == 0 and gate.bias is None)
 
     @classmethod
     def from_members(cls, gate: W4A16Linear, up: W4A16Linear) -> "W4A16SiluGate":

@@ -213,3 +213,35 @@ def test_fused_projections_match_members(tmp_path, fmt):
         assert yf.shape == (2, 3, f.out_features)
         ys = torch.cat([sep[f"model.layers.1.{base}{m}_proj.weight"](x) for m in members], dim=-1)
         torch.testing.assert_close(yf.float(), ys.float(), rtol=2 ** -10, atol=1e-4)
+
+
+@pytest.mark.gpu
+def test_fusion_skipped_when_members_differ(tmp_path):
+    """Members that cannot share one GEMM stay separate linears under their own names:
+    act-order q, k, v (each permuted differently, as desc_act checkpoints are), and q whose
+    zero points are all 8 (dropped at load: symmetric kernels) next to asymmetric k and v."""
+    tensors, dense_w, cfg = _model("gptq", act_order=True, seed=11)
+    arch = str(tmp_path / "act.pulsar")
+    save_archive(arch, cfg, tensors, shards=2)
+    w = load_weights(arch, device="cuda:0", dtype=torch.float16, fuse=True, silu_gate=True)
+    for li in range(2):
+        assert f"model.layers.{li}.self_attn.qkv_proj.weight" not in w
+        assert f"model.layers.{li}.mlp.gate_up_proj.weight" not in w
+    _check_linears(w, dense_w, 5, seed=12)
+
+    tensors, dense_w, cfg = _model("gptq", act_order=False, seed=13)
+    q = "model.layers.0.self_attn.q_proj"
+    kq, nq = HIDDEN, HIDDEN
+    tensors[q + ".qzeros"] = torch.full((kq // G, nq // 8), 0x77777777, dtype=torch.int32)  # v1: z - 1 = 7
+    u = O.unpack_gptq(tensors[q + ".qweight"].numpy()).astype(np.float32)          # [N, K]
+    s = tensors[q + ".scales"].numpy().astype(np.float32)                             # [K/G, N]
+    dense_w[q] = (u - 8.0) * np.repeat(s, G, axis=0).T
+    arch = str(tmp_path / "mixed.pulsar")
+    save_archive(arch, cfg, tensors)
+    w = load_weights(arch, device="cuda:0", dtype=torch.float16, fuse=True)
+    assert w[q + ".weight"].qzeros is None
+    assert "model.layers.0.self_attn.qkv_proj.weight" not in w     # q symmetric, k/v not: separate
+    assert "model.layers.1.self_attn.qkv_proj.weight" in w         # layer 1 fuses as before
+    assert "model.layers.0.mlp.gate_up_proj.weight" in w
+    _check_linears({k: v for k, v in w.items()}, {p: d for p, d in dense_w.items() if "layers.0.self_attn" in p
+                                                  and "o_proj" not in p}, 3, seed=14)

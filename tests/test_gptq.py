@@ -15,15 +15,17 @@ from w4a16_case import baseline_case, check
 pytestmark = pytest.mark.gpu
 
 
-def test_symmetric_gptq_equals_reference_repack():
-    c = baseline_case(1, 256, 512, 128)
+@pytest.mark.parametrize("n,k", [(256, 512), (200, 2176), (1000, 4224)])
+def test_symmetric_gptq_equals_reference_repack(n, k):
+    c = baseline_case(1, n, k, 128)
     wm_ct, _ = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float32), 128)
     wm_gptq, perm = ops.repack_w4a16_gptq(c.qweight(), None, 128)
     assert perm.numel() == 0
     assert torch.equal(wm_ct, wm_gptq)
 
 
-@pytest.mark.parametrize("n,k,g", [(256, 1024, 128), (136, 512, 64), (64, 256, 32), (128, 4096, 128)])
+@pytest.mark.parametrize("n,k,g", [(256, 1024, 128), (136, 512, 64), (64, 256, 32), (128, 4096, 128),
+                                   (200, 2112, 64)])
 def test_act_order_repack_bit_exact(n, k, g):
     c = baseline_case(1, n, k, g, seed=3, symmetric=False, act_order=True)
     g_idx = torch.from_numpy(c.g_idx).cuda()

@@ -247,6 +247,19 @@ def test_gemm_matches_float64(orc):
         assert np.abs(y - ref).max() <= 1e-5 * np.sqrt(k) * np.abs(ref).max() + 1e-5
 
 
+def test_gemm_blas_matches_c_gemm(orc):
+    """The BLAS GEMM the CPU baseline times computes what the C GEMM does."""
+    rng = np.random.default_rng(7)
+    for m, n, k in [(1, 64, 128), (16, 200, 1024), (300, 520, 4096)]:
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        w = rng.standard_normal((n, k)).astype(np.float32)
+        ref = x.astype(np.float64) @ w.astype(np.float64).T
+        yb, yc = orc.gemm_f32_blas(x, w), orc.gemm_f32(x, w)
+        assert yb.shape == (m, n) and yb.dtype == np.float32
+        tol = 1e-5 * np.sqrt(k) * np.abs(ref).max() + 1e-5
+        assert np.abs(yb - ref).max() <= tol and np.abs(yb - yc).max() <= 2 * tol
+
+
 def test_gemm_split_semantics(orc):
     rng = np.random.default_rng(6)
     x = rng.standard_normal((4, 128)).astype(np.float32)  # 2 chunks of 64

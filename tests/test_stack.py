@@ -124,3 +124,35 @@ def test_silu_gated_stack(m):
         torch.testing.assert_close(h.float(), ref, rtol=4e-3, atol=4e-3 * ref.abs().max().item())
         down = gated.layers[0][3]
         torch.testing.assert_close(gated.outputs[3], down(h), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("variant", ["plain", "gated"])
+@pytest.mark.parametrize("m", [1, 32])
+def test_full_32_layer_graph_matches_eager(variant, m):
+    """BASELINE config 5 at its real size: the 32-layer Llama-3-8B stack (224 linears, or
+    128 launches with q|k|v fused and gate|up as the SiLU-gated GEMM feeding down), captured
+    as one graph.  After two replays every output of every launch equals the eager launch
+    on the same inputs, bit for bit; one linear of the last layer is also held to the
+    oracle through its dequantized weights."""
+    layers = random_layers(32, device="cuda:0", seed=9)
+    if variant == "gated":
+        layers = fuse_layers(layers, silu_gate=True)
+    st = W4A16LinearStack(layers, m)
+    st.capture()
+    assert len(st.outputs) == st.launches_per_step() == (224 if variant == "plain" else 128)
+    for _ in range(2):
+        st.step()
+    torch.cuda.synchronize()
+    want = st.forward()
+    torch.cuda.synchronize()
+    for i, (got, ref) in enumerate(zip(st.outputs, want)):
+        assert torch.equal(got, ref), f"{variant} m={m}: launch {i} differs from eager"
+    del want
+    if variant == "plain":
+        # the last layer's k projection (K = 4096, N = 1024) against the oracle
+        lin = layers[-1][1]
+        k, n = lin.in_features, lin.out_features
+        u = O.marlin_to_u(lin.weight_marlin.cpu().numpy(), n, k)
+        w = (u.astype("float32") - 8.0) * lin.scales.float().cpu().numpy().repeat(G, axis=0).T
+        x = st.inputs[k].float().cpu().numpy()
+        check(st.outputs[-6], O.gemm_f32(x, w), torch.float16, f"stack layer 31 k_proj m={m}")
