@@ -198,11 +198,15 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
     const int64_t ktiles = kext / 32;
     const bool forced = num_splits >= 1;
     const bool zp_any = true;  // size the LDS for the asymmetric variant (a few hundred bytes more)
-    const bool decode_ok = M <= 64 && (G == 64 || G % 128 == 0) && (G & (G - 1)) == 0;
+    // The decode kernel takes power-of-two group sizes: 128 K steps hold 128 / G
+    // whole groups (G = 16..64, one masked MFMA per group; G of 16 and 32 up to
+    // M = 32) or lie inside one (G >= 128).
+    const int64_t ngrp = G >= 128 ? 1 : 128 / std::max<int64_t>(G, 1);
+    const bool decode_ok = M <= 64 && G >= 16 && (G & (G - 1)) == 0 && (ngrp <= 2 || M <= 32);
     if (decode_ok) {
         DecodeConfig dc{};
         dc.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-        dc.ngrp = G == 64 ? 2 : 1;
+        dc.ngrp = (int)ngrp;
         const bool bf = x_dtype == PW4_DTYPE_BF16;
         // Columns the units cover (MARLIN pads N to 64; CT columns past N are
         // clamped loads whose results are dropped).
@@ -249,7 +253,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         // M = 5: 11.1 us at 16 against 14.3).
         bool tree = false;
         int tree_nb = 16;
-        if (!forced) {
+        if (!forced && dc.ngrp <= 2) {  // no exchange-tree variants for groups narrower than 64
             int64_t s2 = std::max<int64_t>(s, decode_splits_override());
             if (s2 > 1) {
                 int64_t p2 = 2;
@@ -288,7 +292,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         // steps pad to the ring depth)
         const int64_t kwn = 8 / (nb / 16);
         const int64_t spu = std::max<int64_t>(ceil_div(ceil_div(kps, 128), kwn), 1);
-        dc.ring = spu <= 4 ? 4 : 8;
+        dc.ring = spu <= 4 || dc.ngrp > 2 ? 4 : 8;
         // Persistent grid: one or two workgroups per CU (register and LDS
         // budget), then as few units per workgroup as possible with the
         // least per-CU load.

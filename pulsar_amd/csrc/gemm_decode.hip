@@ -87,22 +87,28 @@ __device__ __forceinline__ void wait_vmcnt() {
 // fp16 B fragment = u - z, exact, for one weight word.  `one` = 0x64006400.
 //   MARLIN (unsigned nibbles): pairs (n_i, n_i+4), i = 0..3.
 //   CT (two's complement): pairs (n_2i, n_2i+1), i.e. natural K order.
+// MARLIN: pair (MFMA) s takes zero point zlo for s < 2 and zhi for s >= 2;
+// they differ only when a quant group is 16 K wide, where MFMAs 0-1 and 2-3 of
+// a lane fall in different groups.  CT: the whole word is one MFMA's K run,
+// so all its pairs take zlo (the caller passes the word's zero point).
 template <int LAYOUT>
-__device__ __forceinline__ u32x4 dq_f16(uint32_t q, uint32_t one, uint32_t z, const NibbleMasks& mk) {
-    const f16x2 z1024 = as_h2((0x6400u | z) * 0x10001u);                 // 1024 + z
-    const f16x2 z64 = as_h2((0x5400u | (z << 4)) * 0x10001u);             // 64 + z
+__device__ __forceinline__ u32x4 dq_f16(uint32_t q, uint32_t one, uint32_t zlo, uint32_t zhi, const NibbleMasks& mk) {
+    const f16x2 z1024_lo = as_h2((0x6400u | zlo) * 0x10001u);             // 1024 + z
+    const f16x2 z64_lo = as_h2((0x5400u | (zlo << 4)) * 0x10001u);        // 64 + z
+    const f16x2 z1024_hi = as_h2((0x6400u | zhi) * 0x10001u);
+    const f16x2 z64_hi = as_h2((0x5400u | (zhi << 4)) * 0x10001u);
     const f16x2 sixteenth = as_h2(0x2c002c00u);
     u32x4 r;
     if constexpr (LAYOUT == LAYOUT_MARLIN) {
         const uint32_t q8 = q >> 8;
-        r[0] = as_u32(as_h2(bfi(mk.lo, q, one)) - z1024);
-        r[1] = as_u32(as_h2(bfi(mk.hi, q, one)) * sixteenth - z64);
-        r[2] = as_u32(as_h2(bfi(mk.lo, q8, one)) - z1024);
-        r[3] = as_u32(as_h2(bfi(mk.hi, q8, one)) * sixteenth - z64);
+        r[0] = as_u32(as_h2(bfi(mk.lo, q, one)) - z1024_lo);
+        r[1] = as_u32(as_h2(bfi(mk.hi, q, one)) * sixteenth - z64_lo);
+        r[2] = as_u32(as_h2(bfi(mk.lo, q8, one)) - z1024_hi);
+        r[3] = as_u32(as_h2(bfi(mk.hi, q8, one)) * sixteenth - z64_hi);
     } else {
         q ^= 0x88888888u;  // two's complement -> u
         const f16x2 mul = as_h2(0x2c003c00u);                                 // {1, 1/16}
-        const f16x2 sub = f16x2{z1024[0], z64[0]};
+        const f16x2 sub = f16x2{z1024_lo[0], z64_lo[0]};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // byte i (nibbles 2i, 2i+1) into bytes 0 and 2, then splice
@@ -111,6 +117,19 @@ __device__ __forceinline__ u32x4 dq_f16(uint32_t q, uint32_t one, uint32_t z, co
         }
     }
     return r;
+}
+
+// Quant group (0 .. NGRP-1) of the K run that lane group h supplies to MFMA s
+// of a 128-K step: MFMA s takes K 32h + 8s .. +8, and a group is 128 / NGRP wide.
+template <int NGRP>
+__host__ __device__ constexpr int step_group(int h, int s) {
+    return ((4 * h + s) * NGRP) >> 4;
+}
+// Whether any lane group of MFMA s falls in group gi (a compile-time fact).
+template <int NGRP>
+__host__ __device__ constexpr bool group_in_mfma(int gi, int s) {
+    return step_group<NGRP>(0, s) == gi || step_group<NGRP>(1, s) == gi || step_group<NGRP>(2, s) == gi ||
+           step_group<NGRP>(3, s) == gi;
 }
 
 // bf16 B fragment = 128 + u (exact), same pair order as dq_f16.
@@ -166,8 +185,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     __shared__ int s_last;
     constexpr int MP = MT * 16;
+    static_assert(NGRP == 1 || NGRP == 2 || NGRP == 4 || NGRP == 8, "quant groups per 128-K step");
     // vector memory instructions per ring step (weights, scales, zero points)
     constexpr int kLoadsPerStep = 1 + NGRP + (ZP ? NGRP : 0);
+    // vmcnt is six bits: waiting for "all but the ring" waits for at most 63
+    // younger loads (with more, a few ring loads are waited for as well)
+    constexpr int kRingLoads = U * kLoadsPerStep < 63 ? U * kLoadsPerStep : 63;
 
     const int tid = threadIdx.x;
     // wave-uniform by construction; readfirstlane tells the compiler, so that
@@ -285,7 +308,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
 
     // ---- finish the slice: zero fill, (bf16) corrections ---------------------
     if constexpr (LAYOUT == LAYOUT_MARLIN) {
-        wait_vmcnt<U * kLoadsPerStep>();  // this wave's slice copies are done; its ring is still in flight
+        wait_vmcnt<kRingLoads>();  // this wave's slice copies are done; its ring is still in flight
     } else {
         wait_vmcnt<0>();
     }
@@ -338,12 +361,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
                 }
             }
         };
+        // lane groups of L <= kChunks lanes
         if (items * kChunks <= kThreads) {
             corr_pass(std::integral_constant<int, kChunks>{});
-        } else if (items * 4 <= kThreads) {
-            corr_pass(std::integral_constant<int, 4>{});
-        } else if (items * 2 <= kThreads) {
-            corr_pass(std::integral_constant<int, 2>{});
+        } else if (kChunks >= 4 && items * 4 <= kThreads) {
+            corr_pass(std::integral_constant<int, (kChunks >= 4 ? 4 : 1)>{});
+        } else if (kChunks >= 2 && items * 2 <= kThreads) {
+            corr_pass(std::integral_constant<int, (kChunks >= 2 ? 2 : 1)>{});
         } else {
             corr_pass(std::integral_constant<int, 1>{});
         }
@@ -362,7 +386,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     int arow[MT];  // A rows past M read row M-1: their D rows are never stored
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) arow[mt] = min(mt * 16 + c, M - 1) * rs + 32 * h;
-    const int my_gi = NGRP == 1 ? 0 : h / 2;
+    // this lane group's quant group in MFMAs 0-1 and in MFMAs 2-3 of a step
+    const int g_lo = step_group<NGRP>(h, 0), g_hi = step_group<NGRP>(h, 2);
 
     auto compute_step = [&](int u, int j, const Step& in) {
         const int st = kw + j * kwn;
@@ -392,9 +417,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
                     tmp[gi][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
                 }
             }
-        uint32_t zsel = zl[0];
+        uint32_t zlo = zl[0], zhi = zl[0];
 #pragma unroll
-        for (int gi = 1; gi < NGRP; ++gi) zsel = my_gi == gi ? zl[gi] : zsel;
+        for (int gi = 1; gi < NGRP; ++gi) {
+            zlo = g_lo == gi ? zl[gi] : zlo;
+            zhi = g_hi == gi ? zl[gi] : zhi;
+        }
         // MARLIN: pair s of word tg holds natural K 8s + 2tg, 8s + 2tg + 1, so
         // pair s of the four words is the contiguous K run [8s, 8s + 8) of the
         // tile, which MFMA s multiplies with natural-order activations.  CT:
@@ -405,7 +433,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
             if constexpr (BF16) {
                 d[w] = dq_bf16<LAYOUT>(in.w[w], one, a.masks);
             } else {
-                d[w] = dq_f16<LAYOUT>(in.w[w], one, zsel, a.masks);
+                if constexpr (LAYOUT == LAYOUT_MARLIN) {
+                    d[w] = dq_f16<LAYOUT>(in.w[w], one, zlo, zhi, a.masks);
+                } else {
+                    const uint32_t zw = w < 2 ? zlo : zhi;  // word w is MFMA w's K run
+                    d[w] = dq_f16<LAYOUT>(in.w[w], one, zw, zw, a.masks);
+                }
             }
         }
 #pragma unroll
@@ -419,11 +452,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const u32x4 av = *reinterpret_cast<const u32x4*>(smem + arow[mt] + kl + 8 * s);
+                // one MFMA per quant group present in MFMA s, each on the lanes of
+                // that group only (the others supply zero activations)
 #pragma unroll
                 for (int gi = 0; gi < NGRP; ++gi) {
+                    if (!group_in_mfma<NGRP>(gi, s)) continue;
                     u32x4 ag = av;
                     if constexpr (NGRP > 1) {
-                        if (my_gi != gi) ag = u32x4{0u, 0u, 0u, 0u};
+                        if ((s < 2 ? g_lo : g_hi) != gi) ag = u32x4{0u, 0u, 0u, 0u};
                     }
                     tmp[gi][mt] = mfma16x16x32<BF16>(ag, b, tmp[gi][mt]);
                 }
@@ -648,17 +684,33 @@ using DecodeFn = void (*)(const DecodeArgs);
 // The exchange tree is a separate instantiation (MT 1 and 2 only: it needs
 // M * 16 <= 512): its atomics in the unit loop make the compiler's wait
 // counts for the weight ring more conservative, which the plain variants
-// should not pay for.
+// should not pay for.  Quant groups narrower than 64 K (NGRP 4 and 8) exist
+// for MT 1 and 2, the 4-step ring and no tree only.
+template <bool BF16, int LAYOUT, typename ST, bool ZP, int U, int MT, bool TREE>
+DecodeFn pick_ngrp(int ngrp) {
+    switch (ngrp) {
+        case 1: return decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE>;
+        case 2: return decode_kernel<BF16, LAYOUT, ST, MT, 2, ZP, U, TREE>;
+        case 4:
+            if constexpr (!TREE && MT <= 2 && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 4, ZP, U, TREE>;
+            return nullptr;
+        case 8:
+            if constexpr (!TREE && MT <= 2 && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 8, ZP, U, TREE>;
+            return nullptr;
+        default: return nullptr;
+    }
+}
+
 template <bool BF16, int LAYOUT, typename ST, bool ZP, int U>
 DecodeFn pick_mt_u(int mt, int ngrp, bool tree) {
     if (tree) {
-        if (mt == 1) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 1, 1, ZP, U, true> : decode_kernel<BF16, LAYOUT, ST, 1, 2, ZP, U, true>;
-        if (mt == 2) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 2, 1, ZP, U, true> : decode_kernel<BF16, LAYOUT, ST, 2, 2, ZP, U, true>;
+        if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, true>(ngrp);
+        if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, true>(ngrp);
         return nullptr;
     }
-    if (mt == 1) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 1, 1, ZP, U, false> : decode_kernel<BF16, LAYOUT, ST, 1, 2, ZP, U, false>;
-    if (mt == 2) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 2, 1, ZP, U, false> : decode_kernel<BF16, LAYOUT, ST, 2, 2, ZP, U, false>;
-    if (mt == 4) return ngrp == 1 ? decode_kernel<BF16, LAYOUT, ST, 4, 1, ZP, U, false> : decode_kernel<BF16, LAYOUT, ST, 4, 2, ZP, U, false>;
+    if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false>(ngrp);
+    if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false>(ngrp);
+    if (mt == 4) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 4, false>(ngrp);
     return nullptr;
 }
 

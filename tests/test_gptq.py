@@ -75,3 +75,30 @@ def test_gptq_gemm_small_groups(m, g):
     scales = torch.from_numpy(np.ascontiguousarray(c.scale_nk.T)).half().cuda()
     y = ops.gemm_w4a16_gptq(c.x, wm, scales, c.qzeros(), perm, g)
     check(y, c.y_ref, torch.float16, f"gptq small groups m={m} g={g}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [1, 5, 16, 32])
+@pytest.mark.parametrize("g", [16, 32])
+@pytest.mark.parametrize("sym,act", [(True, False), (False, False), (False, True)])
+def test_decode_small_groups(m, g, sym, act, dtype):
+    """Group sizes 16 and 32 at decode M run the decode kernel (four or eight quant groups
+    per 128-K step, one masked MFMA per group, zero points per group): against the oracle at
+    a size where K = 4096 spans 128-256 groups and 1000 columns leave a partial column block."""
+    n, k = 1000, 4096
+    c = baseline_case(m, n, k, g, dtype=dtype, seed=9 + g + m, symmetric=sym, act_order=act)
+    g_idx = torch.from_numpy(c.g_idx).cuda() if act else None
+    wm, perm = ops.repack_w4a16_gptq(c.qweight(), g_idx, g)
+    scales = torch.from_numpy(np.ascontiguousarray(c.scale_nk.T)).half().cuda()
+    y = ops.gemm_w4a16_gptq(c.x, wm, scales, None if sym else c.qzeros(), perm if act else None, g)
+    check(y, c.y_ref, dtype, f"decode small groups m={m} g={g} sym={sym} act={act} {dtype}")
+
+
+@pytest.mark.parametrize("m", [1, 8, 24])
+@pytest.mark.parametrize("g", [16, 32])
+def test_decode_small_groups_ct_layout(m, g):
+    """The reference's gemm_w4a16 (compressed-tensors packing, read in place) with G = 16, 32."""
+    n, k = 768, 2048
+    c = baseline_case(m, n, k, g, seed=30 + g + m)
+    y = ops.gemm_w4a16(c.x, c.ct_packed(), c.scale(torch.float32), g)
+    check(y, c.y_ref, torch.float16, f"ct small groups m={m} g={g}")
