@@ -679,10 +679,10 @@ def main() -> int:
     ap.add_argument("--prefill-reps", type=int, default=10)
     ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--no-act-order", action="store_true", help="skip the 70B act-order layers (configs[3])")
-    ap.add_argument("--pmc-workload", choices=["decode", "prefill"],
+    ap.add_argument("--pmc-workload", choices=["decode", "prefill", "prefill-bf16"],
                     help="no timing: decode = the decode sweep's launches once each, then a 512 MiB copy (the "
                          "HBM counter calibration), for rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE; prefill = "
-                         "one M=4096 launch per layer, for MFMA counters")
+                         "one M=4096 launch per layer, for MFMA counters (prefill-bf16: bf16 activations)")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode sweep (headline value null)")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise the two --pmc-workload counter CSVs into profiles/decode_traffic.json")
@@ -717,9 +717,10 @@ def main() -> int:
     def gemm_reference_api(x, w):
         return pulsar_amd.ops.gemm_w4a16_marlin(x, w[0], w[1], G)
 
-    if args.pmc_workload == "prefill":
+    if args.pmc_workload in ("prefill", "prefill-bf16"):
+        xdt = torch.bfloat16 if args.pmc_workload == "prefill-bf16" else torch.float16
         for name, k, n in LLAMA8B:
-            x = torch.randn(PREFILL_M[-1], k, device=dev).half()
+            x = torch.randn(PREFILL_M[-1], k, device=dev).to(xdt)
             gemm_fp16_scales(x, weights[name][0])
         torch.cuda.synchronize()
         return 0

@@ -104,16 +104,19 @@ int decode_splits_override() {
 
 // Plan of the 256-wide prefill kernel: tile rows (256 or 128) and K slices,
 // from a cost model in microseconds fitted to a sweep of every (rows, slices)
-// pair over the Llama-3-8B layer shapes at M = 256..4096 on one MI355X:
-//   * a 64-K chunk of a 256-row tile takes 2.0 us on a CU; 256-row tiles run
-//     one workgroup per CU (126 KB of LDS), in waves of the CU count, and an
-//     unsplit launch balances its last wave with 128-row tiles;
-//   * a 128-row tile's chunk takes 0.6 of that; two such workgroups share a CU
-//     (78 KB of LDS each), which then takes 0.8 of their summed time;
+// pair over the Llama-3-8B and -70B layer shapes at M = 72..4096 on one MI355X
+// (bf16 activations; the fitted picks total 8628 us over 37 shapes against
+// 8617 for the per-shape best and 9185 for the former fp16-fitted model):
+//   * a 64-K chunk of a 256-row tile (8 waves, one workgroup per CU) takes
+//     1.6 us; such tiles run in waves of the CU count, and an unsplit launch
+//     balances its last wave with 128-row tiles;
+//   * 128-row tiles (4 waves) run two workgroups per CU: a chunk takes 1.1 us
+//     on a CU of its own, and a round of two per CU takes 1.6 us;
 //   * K slices add their fp32 partials' round trip, s * M * N * 8 bytes at
-//     6 TB/s, plus 2 us for the combine launch.
-// Picks are within 1% of the sweep's best in total (3682 against 3660 us over
-// 20 shapes; the former fixed rule took 3888).
+//     8 TB/s, plus 1 us for the combine launch.
+// fp16 activations with exact scaling use 128-row tiles only: on the same
+// sweep the model's 128-row picks are within 0.6% of the per-shape best (8367
+// against 8322 us); 256-row tiles were ahead on down_proj of 70B alone, by 1-3%.
 struct Prefill256Plan {
     int rows;
     int64_t splits;
@@ -126,10 +129,11 @@ bool prefill_exact_enabled() {
     return !(e && e[0] == '0');
 }
 
-// only128: 128-row tiles only (the exact-scaling kernel has no 256-row variant);
-// max_splits: the most K slices the plan may use.
+// only128: 128-row tiles only (exact scaling); max_splits: the most K slices
+// the plan may use.
 Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, bool only128, int64_t max_splits) {
-    constexpr double kChunkUs = 2.0, kHalfChunk = 0.6, kShare = 0.8, kPartialBps = 6.0e12, kCombineUs = 2.0;
+    constexpr double kChunk256 = 1.6, kChunk128Solo = 1.1, kChunk128Pair = 1.6, kPartialBps = 8.0e12,
+                     kCombineUs = 1.0;
     Prefill256Plan best{256, 1};
     double best_us = 0.0;
     bool have = false;
@@ -145,10 +149,10 @@ Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, b
             if (rows == 256) {
                 double waves = (double)ceil_div(ceil_div(M, 256) * num_n * s, cus);
                 if (s == 1) prefill256_tail_cols(M, N, cus, &waves);
-                us = waves * (double)cps * kChunkUs;
+                us = waves * (double)cps * kChunk256;
             } else {
                 const int64_t wgs = ceil_div(M, 128) * num_n * s;
-                us = (double)cps * kHalfChunk * kChunkUs * (wgs <= cus ? 1.0 : (double)ceil_div(wgs, cus) * kShare);
+                us = (double)cps * (wgs <= cus ? kChunk128Solo : (double)ceil_div(wgs, 2 * (int64_t)cus) * kChunk128Pair);
             }
             if (s > 1) us += (double)s * (double)M * (double)N * 8.0 / kPartialBps * 1e6 + kCombineUs;
             if (!have || us < best_us) {
@@ -390,7 +394,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         p.use_partial = forced || s > 1;
         if (p.use_partial) p.partial_bytes = (size_t)p.splits * M * N * 4;
         if (p.p256 && prefill_rows_override()) p.p_tile_rows = prefill_rows_override();
-        if (p.p_exact) p.p_tile_rows = 128;
+        if (p.p_exact && !prefill_rows_override()) p.p_tile_rows = 128;
     }
     // act-order: x is gathered once per call into the workspace, for either
     // kernel (each decode workgroup would otherwise gather the same slice)

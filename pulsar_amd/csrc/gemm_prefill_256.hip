@@ -1,16 +1,18 @@
-// Compute-bound W4A16 GEMM for large M on the MARLIN layout with fp16
-// activations: y[M,N] = x[M,K] @ dequant(W)^T, 256 x 256 output tile per
-// workgroup.
+// Compute-bound W4A16 GEMM for large M on the MARLIN layout with fp16 or
+// bf16 activations: y[M,N] = x[M,K] @ dequant(W)^T, one 256-column output
+// tile of 256 or 128 rows per workgroup.
 //
-// Tiling.  Four waves; wave w owns MARLIN column block w of the tile (64
-// columns) for all 256 rows: 8 x 2 tiles of v_mfma_f32_32x32x16_f16 with the
-// fp32 accumulators in AGPRs.  Splitting the tile by columns means every
-// weight nibble is dequantized exactly once per workgroup; the activation
-// tile is read from LDS by all four waves instead.  K advances in 64-wide
-// chunks (one MARLIN chunk per column block).
+// Tiling.  256-row tiles: eight waves; waves 2b and 2b + 1 own the two
+// 32-column halves of MARLIN column block b (64 columns) for all 256 rows,
+// 8 tiles of v_mfma_f32_32x32x16 each.  128-row tiles: four waves; wave w owns
+// column block w for all 128 rows, 4 x 2 tiles.  Either way a wave holds 128
+// fp32 accumulators per lane in VGPRs, two waves share a SIMD, every weight
+// nibble is dequantized exactly once per workgroup, and the activation tile
+// is read from LDS by every wave.  K advances in 64-wide chunks (one MARLIN
+// chunk per column block).
 //
-// Pipeline.  Three LDS stages of (activations 32 KB, packed weights 8 KB,
-// scales, zero points), filled with global_load_lds (no VGPRs; each lane
+// Pipeline.  Three LDS stages of (activations 32 or 16 KB, packed weights
+// 8 KB, scales, zero points), filled with global_load_lds (no VGPRs; each lane
 // names its own global address, the 64 lanes of an instruction fill 64
 // consecutive LDS elements).  The copies are issued from inline assembly so
 // that the compiler does not serialise them: it would otherwise wait for
@@ -26,8 +28,9 @@
 // Dequant.  Pair p of MARLIN word tg (nibbles p, p+4) holds natural K
 // {8p + 2tg, 8p + 2tg + 1}, so pair p of a column's four words is the K run
 // [8p, 8p + 8) -- exactly what one lane supplies to an MFMA.  fp16 x, per
-// pair: shift, splice into 1024.0 (exact 1024 + u), subtract 1024 + z
-// (exact), times the group scale (one fp16 rounding, as the reference's
+// pair: splice into 1024.0 or 64.0 (exact 1024 + u or 64 + u, by the pair's
+// bit position), subtract 1024 + z or 64 + z (exact), and -- unless scaling
+// exactly -- times the group scale (one fp16 rounding, as the reference's
 // dequant_scale, w4a16_marlin.cu:103-113).  bf16 x (gfx950 has no packed bf16
 // arithmetic): splice into 128.0 (exact 128 + u), then per value one fp32 fma
 // (128 + u) * s - (128 + z) * s with s the scale rounded to bf16 -- both
@@ -35,19 +38,20 @@
 // reference's bf16 fragment round(q * round(s)) bit for bit
 // (w4a16_marlin.cu:115-126).
 //
-// Exact scaling (fp16 x, 128-row tiles).  Rounding (u - z) * s to fp16 costs
-// up to 2^-11 of every weight; summed over K = 14336-28672 that is ~1e-2 of
+// Exact scaling (fp16 x, the default).  Rounding (u - z) * s to fp16 costs up
+// to 2^-11 of every weight; summed over K = 14336-28672 that is ~1e-2 of
 // absolute error at the BASELINE magnitudes.  In this mode B = u - z (exact in
 // fp16) and the group scale is applied in fp32 to the accumulators instead:
 // with s_g the scale of group g for the lane's column, the running sum is
 // rescaled by s_(g-1) / s_g when group g starts and multiplied by the last
 // group's scale at the end, so acc = sum_g s_g * P_g with P_g the exact
-// fp32 sum of group g.  One multiply per accumulator per group (the
-// accumulators are VGPRs here), and no second accumulator set.
+// fp32 sum of group g.  One multiply per accumulator per group, and no second
+// accumulator set.
 //
 // Reference counterpart: w4a16_marlin_kernel at BM = 64
 // (pulsar-core/src/kernels/w4a16_marlin.cu:197-304).
 #include <algorithm>
+#include <type_traits>
 
 #include "w4a16_common.h"
 #include "w4a16_kernels.h"
@@ -55,42 +59,41 @@
 namespace pw4 {
 namespace {
 
-constexpr int kT = 256;
 constexpr int TM = 256, TN = 256, TK = 64;  // full tile; the tail variant has TM = 128
 constexpr int kStages = 3;
 constexpr int kBStage = TN * TK / 2;
-constexpr int kSStage = 4 * 256;      // per wave 256 bytes of scales (64 fp32, or 64 fp16 + pad)
-constexpr int kZStage = 4 * 256;      // per wave 256 bytes of zero-point words (8 used)
+constexpr int kSlot = 256;  // per wave and stage: 256 bytes of scales (64 fp32, or 64 fp16 + pad), of zero-point words
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)p;
 }
 
-// One LDS copy instruction: lane l copies 16 (or 4) bytes from g to
+// One LDS copy instruction: lane l copies 16 (or 4) bytes from base + off
+// (base wave-uniform in SGPRs, off a 32-bit per-lane byte offset) to
 // LDS[lds + l * 16 (or 4)].  M0 (the LDS base) is saved and restored around
 // it; the s_nop covers the M0-write -> LDS-DMA hazard.
-__device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds) {
+__device__ __forceinline__ void lds_copy16(const void* base, uint32_t off, uint32_t lds) {
     uint32_t saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
+        "s_mov_b32 m0, %3\n\t"
         "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, off\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "v"(g), "s"(lds)
+        : "v"(off), "s"(base), "s"(lds)
         : "memory");
 }
-__device__ __forceinline__ void lds_copy4(const void* g, uint32_t lds) {
+__device__ __forceinline__ void lds_copy4(const void* base, uint32_t off, uint32_t lds) {
     uint32_t saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
+        "s_mov_b32 m0, %3\n\t"
         "s_nop 0\n\t"
-        "global_load_lds_dword %1, off\n\t"
+        "global_load_lds_dword %1, %2\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "v"(g), "s"(lds)
+        : "v"(off), "s"(base), "s"(lds)
         : "memory");
 }
 
@@ -109,28 +112,38 @@ __device__ __forceinline__ float exact_scale(float s) {
     return __builtin_fabsf(s) < kMinScale ? __builtin_copysignf(kMinScale, s) : s;
 }
 
-// RT = 32-row MFMA tiles per wave: 8 (256-row tile) or 4 (128-row tile, for
-// the N columns of the last wave, every tile of a 128-row plan, and exact
-// scaling; see launch_prefill256).
-// 128-row tiles (RT = 4) use 78 KB of LDS, so two workgroups fit on a CU if
-// each wave keeps to 256 registers (two waves per SIMD).
-template <bool BF16, typename ST, bool ZP, bool PARTIAL, int RT, bool EXACT = false>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(RT == 4 ? 2 : 1, RT == 4 ? 2 : 1)))
+// RT = 32-row MFMA tiles per wave, and the number of waves: 4 (128-row tile:
+// wave w owns MARLIN column block w, two column tiles of 32) or 8 (256-row
+// tile: waves 2b and 2b + 1 own the two 32-column halves of block b, so each
+// wave dequantizes only its own columns).  Either way 128 fp32 accumulators
+// per lane, kept in VGPRs, and two waves per SIMD (256 registers each):
+// 128-row tiles (75-78 KB of LDS) run two workgroups per CU, 256-row tiles
+// (123-132 KB) one.
+template <bool BF16, typename ST, bool ZP, bool PARTIAL, int RT, bool EXACT>
+__global__ __launch_bounds__(64 * RT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
-    static_assert(!EXACT || (!BF16 && RT == 4), "exact scaling: fp16 activations, 128-row tiles");
+    static_assert(RT == 4 || RT == 8, "128- or 256-row tiles");
+    static_assert(!EXACT || !BF16, "exact scaling: fp16 activations");
+    constexpr int NW = RT;                       // waves
+    constexpr int CT = 8 / RT;                   // 32-column MFMA tiles per wave
+    constexpr int WPB = NW / 4;                  // waves per 64-column block
     constexpr int TMR = 32 * RT;                 // rows of this tile
     constexpr int kAStage = TMR * TK * 2;        // bytes
+    constexpr int kARows = TMR / NW;             // activation rows each wave copies
+    constexpr int kACopies = kARows / 8;         // one copy instruction moves 8 rows of 128 bytes
+    constexpr int kBCopies = 2 / WPB;            // the block's two 1 KB weight tiles, shared by its waves
     __shared__ __attribute__((aligned(16))) uint8_t sA[kStages][kAStage];
     __shared__ __attribute__((aligned(16))) uint8_t sB[kStages][kBStage];
-    __shared__ __attribute__((aligned(16))) uint8_t sS[kStages][kSStage];
-    __shared__ __attribute__((aligned(16))) uint8_t sZ[kStages][kZStage];
-    // copies per wave per chunk: RT activation, 2 weight, 1 scale, 1 zero point
-    constexpr int kCopies = RT + 2 + 1 + (ZP ? 1 : 0);
+    __shared__ __attribute__((aligned(16))) uint8_t sS[kStages][NW * kSlot];
+    __shared__ __attribute__((aligned(16))) uint8_t sZ[kStages][ZP ? NW * kSlot : 16];
+    // copies per wave per chunk: activations, weights, 1 scale, 1 zero point
+    constexpr int kCopies = kACopies + kBCopies + 1 + (ZP ? 1 : 0);
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int c = lane & 31, hb = lane >> 5;
+    const int cbl = wave / WPB, cth = wave % WPB;  // column block of the tile, 32-column half (8 waves)
     const int M = a.M, N = a.N, K = a.K;
 
     // ---- tile order: XCD-aware, then grouped along M for L2 reuse ----------
@@ -153,99 +166,119 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
     const int nck = max(c_end - c_begin, 0);
 
     const int ncb = (N + 63) / 64;              // MARLIN column blocks present
-    const int cbw = min(n0 / 64 + wave, ncb - 1);  // this wave's block (clamped: junk columns are never stored)
-    const int ncol0 = n0 + wave * 64;           // first column of this wave
+    const int cbw = min(n0 / 64 + cbl, ncb - 1);  // this wave's block (clamped: junk columns are never stored)
+    const int ncol0 = n0 + cbl * 64;            // first column of this wave's block
     const ST* scales = reinterpret_cast<const ST*>(a.scales);
 
     // ---- copies of one chunk into a stage (unconditional: constant count) ---
+    // Per-lane byte offsets are fixed for the whole K loop; the bases move.
     // Rows past M, columns past N read clamped addresses; their results are
-    // never stored.
-    auto issue = [&](int kc, int st) {
-        const uint32_t abase = lds_addr(&sA[st][0]) + wave * RT * 1024;
+    // never stored.  Offsets stay below 2^32: prefill256_ok bounds K.
+    uint32_t a_off[kACopies];
 #pragma unroll
-        for (int i = 0; i < RT; ++i) {
-            const int row = wave * (8 * RT) + i * 8 + (lane >> 3);
-            const int kch = (lane & 7) ^ ((row >> 1) & 7);
-            const int gm = min(m0 + row, M - 1);
-            lds_copy16(a.x + (int64_t)gm * K + kc * TK + kch * 8, abase + i * 64 * 16);
-        }
+    for (int i = 0; i < kACopies; ++i) {
+        const int row = wave * kARows + i * 8 + (lane >> 3);
+        const int kch = (lane & 7) ^ ((row >> 1) & 7);
+        a_off[i] = (uint32_t)((min(m0 + row, M - 1) - m0) * K + kch * 8) * 2u;
+    }
+    const uint32_t s_off = sizeof(ST) == 4 ? (uint32_t)min(ncol0 + lane, N - 1) * 4u
+                                           : (uint32_t)min(ncol0 + 2 * lane, N - 2) * 2u;  // N even
+    const int nw = N / 8;
+    const uint32_t z_off = (uint32_t)min(ncol0 / 8 + lane, nw - 1) * 4u;
+    const uint16_t* x_tile = a.x + (int64_t)m0 * K;
+    auto issue = [&](int kc, int st, int g) {
+        const uint32_t abase = lds_addr(&sA[st][0]) + wave * kARows * 128;
+#pragma unroll
+        for (int i = 0; i < kACopies; ++i) lds_copy16(x_tile + kc * TK, a_off[i], abase + i * 1024);
         const uint32_t* wsrc = a.w + ((int64_t)cbw * a.nchunks + kc) * kChunkWords;
-        const uint32_t bbase = lds_addr(&sB[st][0]) + wave * 2048;
+        const uint32_t bbase = lds_addr(&sB[st][0]) + cbl * 2048;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) lds_copy16(wsrc + (i * 64 + lane) * 4, bbase + i * 1024);
-        const int g = min(kc * TK / a.G, a.Kg - 1);
-        const uint32_t sbase = lds_addr(&sS[st][0]) + wave * 256;
-        if constexpr (sizeof(ST) == 4) {
-            lds_copy4(scales + (int64_t)g * N + min(ncol0 + lane, N - 1), sbase);
-        } else {
-            lds_copy4(scales + (int64_t)g * N + min(ncol0 + 2 * lane, N - 2), sbase);  // N even
+        for (int i = 0; i < kBCopies; ++i) {
+            const int tt = cth * kBCopies + i;
+            lds_copy16(wsrc, (uint32_t)(tt * 64 + lane) * 16u, bbase + tt * 1024);
         }
-        if constexpr (ZP) {
-            const int nw = N / 8;
-            lds_copy4(a.qzeros + (int64_t)g * nw + min(ncol0 / 8 + lane, nw - 1), lds_addr(&sZ[st][0]) + wave * 256);
-        }
+        lds_copy4(scales + (int64_t)g * N, s_off, lds_addr(&sS[st][0]) + wave * kSlot);
+        if constexpr (ZP) lds_copy4(a.qzeros + (int64_t)g * nw, z_off, lds_addr(&sZ[st][0]) + wave * kSlot);
     };
 
-    f32x16 acc[RT][2];
+    f32x16 acc[RT][CT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
+        for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[rt][ct][e] = 0.f;
 
-    // splice constant in a VGPR (the mask comes in an SGPR): one v_and_or_b32
-    uint32_t one;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(one) : "s"(BF16 ? 0x43004300u : 0x64006400u));
+    // Dequant constants.  fp16: the lane's nibble pair sits at bit 4 * hb of
+    // each half-word on even steps (at 8 + 4 * hb on odd steps, shifted down by
+    // 8 first).  At bit 0 it is spliced into 1024.0 (0x6400: exact 1024 + u),
+    // at bit 4 into 64.0 (0x5400: mantissa 16u is exact 64 + u), so an even
+    // step needs no shift.  bf16: spliced into 128.0 after a shift.  Masks and
+    // splice constants live in VGPRs, which gives one v_and_or_b32 each.
+    uint32_t one, msk;
+    if constexpr (BF16) {
+        asm volatile("v_mov_b32 %0, %1" : "=v"(one) : "s"(0x43004300u));
+        msk = mk.lo;
+    } else {
+        one = hb ? 0x54005400u : 0x64006400u;
+        msk = hb ? mk.hi : mk.lo;
+        asm volatile("" : "+v"(one), "+v"(msk));  // opaque: keeps one v_and_or_b32 per word
+    }
+    const uint32_t zsplice = hb ? 0x5400u : 0x6400u, zsh = 4u * hb;
 
     // exact mode: the effective scale of the group the accumulators are in,
     // per column tile (1 until the first chunk; an empty slice stores 0 * 1)
-    float s_run[2] = {1.f, 1.f};
+    float s_run[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) s_run[ct] = 1.f;
 
     // One chunk = four 16-K steps; step s is pair s % 2 of 32-K tile s / 2, and
     // this lane's K run in it is [16s + 8hb, +8): activation 16-byte unit
-    // 2s + hb, weight nibble pair 2(s % 2) + hb.  Operands of step s + 1 (eight
-    // A fragments, the dequantized B) are fetched while step s's 16 MFMAs run.
+    // 2s + hb, weight nibble pair 2(s % 2) + hb.  Operands of step s + 1 (the
+    // A fragments, the dequantized B) are fetched while step s's MFMAs run.
     // new_group (exact mode): this chunk starts a quant group after another one.
     auto compute = [&](int st, bool new_group) {
         const uint8_t* A = &sA[st][0];
-        const uint8_t* B = &sB[st][0] + wave * 2048;
-        u32x4 wq[2][2];
+        const uint8_t* B = &sB[st][0] + cbl * 2048;
+        u32x4 wq[2][CT];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) wq[t][ct] = *reinterpret_cast<const u32x4*>(B + t * 1024 + (ct * 32 + c) * 16);
-        f16x2 s2[2], z2[2];   // fp16: scale, 1024 + z
-        float sb[2], cz[2];   // bf16: scale rounded to bf16, -(128 + z) * scale
+            for (int ct = 0; ct < CT; ++ct)
+                wq[t][ct] = *reinterpret_cast<const u32x4*>(B + t * 1024 + ((cth * CT + ct) * 32 + c) * 16);
+        f16x2 s2[CT];
+        uint32_t z2[CT];     // fp16: the zero point spliced like the nibbles (1024 + z or 64 + z)
+        float sb[CT], cz[CT];  // bf16: scale rounded to bf16, -(128 + z) * scale
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            const int cl = ct * 32 + c;  // column inside the wave's block
+        for (int ct = 0; ct < CT; ++ct) {
+            const int cl = (cth * CT + ct) * 32 + c;  // column inside the block
             float sf;
             if constexpr (sizeof(ST) == 4) {
-                sf = *reinterpret_cast<const float*>(&sS[st][wave * 256 + cl * 4]);
+                sf = *reinterpret_cast<const float*>(&sS[st][wave * kSlot + cl * 4]);
             } else {
-                sf = (float)*reinterpret_cast<const _Float16*>(&sS[st][wave * 256 + cl * 2]);
+                sf = (float)*reinterpret_cast<const _Float16*>(&sS[st][wave * kSlot + cl * 2]);
             }
             uint32_t z = 8u;
-            if constexpr (ZP) z = (*reinterpret_cast<const uint32_t*>(&sZ[st][wave * 256 + (cl >> 3) * 4]) >> (4 * (cl & 7))) & 0xfu;
+            if constexpr (ZP) z = (*reinterpret_cast<const uint32_t*>(&sZ[st][wave * kSlot + (cl >> 3) * 4]) >> (4 * (cl & 7))) & 0xfu;
             if constexpr (BF16) {
                 sb[ct] = (float)(__bf16)sf;
                 cz[ct] = -(128.f + (float)z) * sb[ct];
-            } else if constexpr (EXACT) {
-                z2[ct] = as_h2((0x6400u | z) * 0x10001u);  // 1024 + z
-                const float se = exact_scale(sf);
-                if (new_group) {
-                    const float r = s_run[ct] / se;
-#pragma unroll
-                    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-                        for (int e = 0; e < 16; ++e) acc[rt][ct][e] *= r;
-                }
-                s_run[ct] = se;
             } else {
-                const _Float16 sh = (_Float16)sf;
-                s2[ct] = f16x2{sh, sh};
-                z2[ct] = as_h2((0x6400u | z) * 0x10001u);  // 1024 + z
+                z2[ct] = (zsplice | (z << zsh)) * 0x10001u;
+                if constexpr (EXACT) {
+                    const float se = exact_scale(sf);
+                    if (new_group) {
+                        const float r = s_run[ct] * __builtin_amdgcn_rcpf(se);
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                            for (int e = 0; e < 16; ++e) acc[rt][ct][e] *= r;
+                    }
+                    s_run[ct] = se;
+                } else {
+                    const _Float16 sh = (_Float16)sf;
+                    s2[ct] = f16x2{sh, sh};
+                }
             }
         }
         auto load_a = [&](int s, u32x4 (&av)[RT]) {
@@ -256,25 +289,24 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
                 av[rt] = *reinterpret_cast<const u32x4*>(A + row * (TK * 2) + ((kch ^ ((row >> 1) & 7)) * 16));
             }
         };
-        auto dequant = [&](int s, u32x4 (&bv)[2]) {
-            const int sh = 8 * (s & 1) + 4 * hb;
+        auto dequant = [&](int s, u32x4 (&bv)[CT]) {
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
+            for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
                 for (int tg = 0; tg < 4; ++tg) {
-                    const uint32_t v = ((wq[s >> 1][ct][tg] >> sh) & mk.lo) | one;
                     if constexpr (BF16) {
+                        const uint32_t v = ((wq[s >> 1][ct][tg] >> (8 * (s & 1) + 4 * hb)) & msk) | one;
                         bv[ct][tg] = pack_bf16x2_rne(__builtin_fmaf(__builtin_bit_cast(float, v << 16), sb[ct], cz[ct]),
                                                      __builtin_fmaf(__builtin_bit_cast(float, v & 0xffff0000u), sb[ct],
                                                                     cz[ct]));
-                    } else if constexpr (EXACT) {
-                        bv[ct][tg] = as_u32(as_h2(v) - z2[ct]);  // u - z, exact
                     } else {
-                        bv[ct][tg] = as_u32((as_h2(v) - z2[ct]) * s2[ct]);
+                        const uint32_t w = (s & 1) ? wq[s >> 1][ct][tg] >> 8 : wq[s >> 1][ct][tg];
+                        const f16x2 u = as_h2((w & msk) | one) - as_h2(z2[ct]);  // u - z, exact
+                        bv[ct][tg] = EXACT ? as_u32(u) : as_u32(u * s2[ct]);
                     }
                 }
         };
-        u32x4 av[2][RT], bv[2][2];
+        u32x4 av[2][RT], bv[2][CT];
         load_a(0, av[0]);
         dequant(0, bv[0]);
 #pragma unroll
@@ -287,46 +319,47 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = mfma32x32x16<BF16>(av[cur][rt], bv[cur][ct], acc[rt][ct]);
-            // interleave (256-row tiles, one workgroup per CU): per A fragment of
-            // the next step, two MFMAs and its dequant share.  128-row tiles run
-            // two workgroups per CU, whose waves cover each other's latency; the
-            // compiler's own schedule is faster there (measured 3-10%).
-            if (RT == 8 && s < 3) {
-#pragma unroll
-                for (int i = 0; i < RT; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);         // DS read
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, (BF16 ? 56 : 32) / RT, 0);  // VALU
-                }
-            }
+                for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = mfma32x32x16<BF16>(av[cur][rt], bv[cur][ct], acc[rt][ct]);
+            // (two waves per SIMD cover each other's latency; the compiler's own
+            // schedule beat an explicit MFMA / DS read / VALU interleave by 3-10%)
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    if (nck > 0) issue(c_begin, 0);
-    if (nck > 1) issue(c_begin + 1, 1);
-    // position of the chunk in its quant group (G is a multiple of 64)
+    // quant group of the next chunk to issue, and the chunk's place in it (G is
+    // a multiple of 64); issues run in chunk order
     const int cpg = a.G / TK;
-    int gk = EXACT ? c_begin % cpg : 0;
+    int ig = c_begin / cpg, igk = c_begin - ig * cpg;
+    auto next_group = [&]() {
+        const int g = min(ig, a.Kg - 1);
+        if (++igk == cpg) {
+            igk = 0;
+            ++ig;
+        }
+        return g;
+    };
+    if (nck > 0) issue(c_begin, 0, next_group());
+    if (nck > 1) issue(c_begin + 1, 1, next_group());
+    int gk = EXACT ? c_begin % cpg : 0;  // place of the chunk being computed in its group
+    int st = 0, st2 = 2;                 // stages of chunks i and i + 2
     for (int i = 0; i < nck; ++i) {
-        const int st = i % kStages;
         if (i + 1 < nck) {
             wait_vmcnt<kCopies>();  // this wave's copies of chunk i have landed
         } else {
             wait_vmcnt<0>();
         }
         __syncthreads();            // everyone's have; everyone is done with chunk i - 1
-        if (i + 2 < nck) issue(c_begin + i + 2, (i + 2) % kStages);
+        if (i + 2 < nck) issue(c_begin + i + 2, st2, next_group());
         compute(st, i > 0 && gk == 0);
         if constexpr (EXACT) gk = gk + 1 == cpg ? 0 : gk + 1;
+        st = st == kStages - 1 ? 0 : st + 1;
+        st2 = st2 == kStages - 1 ? 0 : st2 + 1;
     }
     if constexpr (EXACT) {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
+            for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[rt][ct][e] *= s_run[ct];
     }
@@ -345,8 +378,8 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
             const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(a.y + (int64_t)m0 * nh, (short)0,
                                                                                 rows * nh * 2, 0x00020000);
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                const int n = ncol0 + ct * 32 + c;
+            for (int ct = 0; ct < CT; ++ct) {
+                const int n = ncol0 + (cth * CT + ct) * 32 + c;
                 const int on = (n >> 4 << 3) | (n & 7);
                 const uint32_t base = (n < N && (c & 8) == 0) ? (uint32_t)(4 * hb * nh + on) * 2u : 0x80000000u;
 #pragma unroll
@@ -367,8 +400,8 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
         const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(a.y + (int64_t)m0 * N, (short)0,
                                                                             rows * N * 2, 0x00020000);
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            const int n = ncol0 + ct * 32 + c;
+        for (int ct = 0; ct < CT; ++ct) {
+            const int n = ncol0 + (cth * CT + ct) * 32 + c;
             const uint32_t base = n < N ? (uint32_t)(4 * hb * N + n) * 2u : 0x80000000u;
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
@@ -386,8 +419,8 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
         const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
             a.partial + ((int64_t)split * M + m0) * N, (short)0, rows * N * 4, 0x00020000);
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            const int n = ncol0 + ct * 32 + c;
+        for (int ct = 0; ct < CT; ++ct) {
+            const int n = ncol0 + (cth * CT + ct) * 32 + c;
             const uint32_t base = n < N ? (uint32_t)(4 * hb * N + n) * 4u : 0x80000000u;
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
@@ -411,8 +444,9 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
 bool prefill256_ok(int layout, int xtype, int64_t N, int64_t K, int64_t G) {
     // 32-bit buffer offsets: a 256-row fp32 partial tile of the output must
     // stay below 2 GiB
+    // 32-bit per-lane activation offsets inside a 256-row tile: 256 * K * 2 bytes
     return layout == LAYOUT_MARLIN && (xtype == X_F16 || xtype == X_BF16) && K % TK == 0 && G % TK == 0 && N % 8 == 0 &&
-           N <= (int64_t{1} << 20);
+           N <= (int64_t{1} << 20) && K <= (int64_t{1} << 22);
 }
 
 int prefill256_tile() { return TM; }
@@ -453,32 +487,32 @@ void launch_variant(const PrefillArgs& a, hipStream_t stream, KernelEvents ev) {
     PrefillArgs w = a;  // a launch over every column of the output
     w.n_begin = 0;
     w.n_end = a.N;
-    if constexpr (!BF16) {
-        if (a.exact) {  // exact scaling: 128-row tiles only (the plan asks for no others)
-            const dim3 grid((unsigned)tiles128, 1, a.partial != nullptr ? a.splits : 1);
-            if (a.partial != nullptr) {
-                launch_kernel(prefill256_kernel<false, ST, ZP, true, 4, true>, grid, dim3(kT), 0, stream, ev.start,
-                              ev.stop, w, mk);
-            } else {
-                launch_kernel(prefill256_kernel<false, ST, ZP, false, 4, true>, grid, dim3(kT), 0, stream, ev.start,
-                              ev.stop, w, mk);
+    const bool exact = !BF16 && a.exact;
+    auto launch = [&](auto rt, dim3 grid, const PrefillArgs& args, hipEvent_t start, hipEvent_t stop, auto partial) {
+        constexpr int RT = decltype(rt)::value;
+        constexpr bool P = decltype(partial)::value;
+        if constexpr (!BF16) {
+            if (exact) {
+                launch_kernel(prefill256_kernel<false, ST, ZP, P, RT, true>, grid, dim3(64 * RT), 0, stream, start,
+                              stop, args, mk);
+                return;
             }
-            return;
         }
-    }
+        launch_kernel(prefill256_kernel<BF16, ST, ZP, P, RT, false>, grid, dim3(64 * RT), 0, stream, start, stop, args,
+                      mk);
+    };
+    auto full = [&](auto... v) { launch(std::integral_constant<int, 8>{}, v...); };
+    auto half = [&](auto... v) { launch(std::integral_constant<int, 4>{}, v...); };
     if (a.partial != nullptr) {  // K slices: fp32 partials of 256- or 128-row tiles
         if (a.tile_rows == TM / 2) {
-            launch_kernel(prefill256_kernel<BF16, ST, ZP, true, 4>, dim3((unsigned)tiles128, 1, a.splits), dim3(kT), 0,
-                          stream, ev.start, ev.stop, w, mk);
+            half(dim3((unsigned)tiles128, 1, a.splits), w, ev.start, ev.stop, std::true_type{});
         } else {
-            launch_kernel(prefill256_kernel<BF16, ST, ZP, true, 8>, dim3((unsigned)(num_m * num_n), 1, a.splits),
-                          dim3(kT), 0, stream, ev.start, ev.stop, w, mk);
+            full(dim3((unsigned)(num_m * num_n), 1, a.splits), w, ev.start, ev.stop, std::true_type{});
         }
         return;
     }
     if (a.tile_rows == TM / 2) {  // every tile 128 rows: twice the workgroups, two per CU
-        launch_kernel(prefill256_kernel<BF16, ST, ZP, false, 4>, dim3((unsigned)tiles128), dim3(kT), 0, stream,
-                      ev.start, ev.stop, w, mk);
+        half(dim3((unsigned)tiles128), w, ev.start, ev.stop, std::false_type{});
         return;
     }
     const int64_t nt = prefill256_tail_cols(a.M, a.N, a.cus, nullptr);
@@ -487,15 +521,14 @@ void launch_variant(const PrefillArgs& a, hipStream_t stream, KernelEvents ev) {
         PrefillArgs f = a;
         f.n_begin = 0;
         f.n_end = (int)std::min<int64_t>(a.N, nfull * TN);
-        launch_kernel(prefill256_kernel<BF16, ST, ZP, false, 8>, dim3((unsigned)(num_m * nfull)), dim3(kT), 0, stream,
-                      ev.start, nt > 0 ? nullptr : ev.stop, f, mk);
+        full(dim3((unsigned)(num_m * nfull)), f, ev.start, nt > 0 ? nullptr : ev.stop, std::false_type{});
     }
     if (nt > 0) {
         PrefillArgs h = a;
         h.n_begin = (int)(nfull * TN);
         h.n_end = a.N;
-        launch_kernel(prefill256_kernel<BF16, ST, ZP, false, 4>, dim3((unsigned)(ceil_div(a.M, TM / 2) * nt)), dim3(kT),
-                      0, stream, nfull > 0 ? nullptr : ev.start, ev.stop, h, mk);
+        half(dim3((unsigned)(ceil_div(a.M, TM / 2) * nt)), h, nfull > 0 ? nullptr : ev.start, ev.stop,
+             std::false_type{});
     }
 }
 

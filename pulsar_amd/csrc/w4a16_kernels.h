@@ -132,7 +132,7 @@ struct PrefillArgs {
     int tile_rows;           // 256-wide kernel: 256-row tiles (tail balanced when unsplit) or 128-row tiles
     int silu;                // 256-wide kernel, unsplit: y [M, N/2] = silu(gate) * up (see DecodeArgs)
     int exact;               // 256-wide kernel, fp16 x: B = u - z and the scale applied to the fp32
-                             // accumulators per group (128-row tiles only)
+                             // accumulators per group
 };
 
 hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream,

@@ -108,11 +108,11 @@ def test_prefill_tail_split(plan_env):
 @pytest.mark.parametrize("splits", [1, 3, 8])
 @pytest.mark.parametrize("m,n", [(300, 520), (129, 264)])
 def test_prefill_plans_agree_with_oracle(plan_env, exact, rows, splits, m, n):
-    """Every plan the 256-wide kernel can be given -- 256- or 128-row tiles,
-    unsplit (with 128-row tail tiles) or with K slices, exact scaling (the
-    default for fp16 x, 128-row tiles whatever the override) or the scale
-    rounded into the fp16 B fragment -- computes the same GEMM: ragged M and N
-    against the oracle, fp16 and fp32 scales."""
+    """Every plan the 256-wide kernel can be given -- 256-row tiles (8 waves)
+    or 128-row tiles (4 waves), unsplit (with 128-row tail tiles) or with K
+    slices, exact scaling (the default for fp16 x) or the scale rounded into
+    the fp16 B fragment -- computes the same GEMM: ragged M and N against the
+    oracle, fp16 and fp32 scales."""
     k, g = 1024, 128
     plan_env["PW4_PREFILL_ROWS"] = str(rows)
     plan_env["PW4_PREFILL_SPLITS"] = str(splits)
@@ -166,3 +166,24 @@ def test_prefill_bf16_kernels_agree():
             del os.environ["PW4_PREFILL_TILE"]
     diff = (ys[128] - ys[256]).abs().max().item()
     assert diff <= 1e-2 * ys[128].abs().max().item(), diff
+
+
+@pytest.mark.parametrize("dtype,exact", [(torch.float16, "1"), (torch.float16, "0"), (torch.bfloat16, "0")],
+                         ids=["f16-exact", "f16-rounded", "bf16"])
+@pytest.mark.parametrize("splits", [1, 2])
+def test_prefill_tile_shapes_bit_identical(plan_env, dtype, exact, splits):
+    """256-row tiles (8 waves, one 32-column tile each) and 128-row tiles (4
+    waves, two column tiles each) feed every output element the same B fragments
+    and A rows through the same MFMA sequence (and, in exact mode, the same
+    rescale points): the outputs are bit-identical."""
+    m, n, k, g = 700, 1032, 2048, 128
+    c = reference_case(m, n, k, g, dtype, seed=20)
+    wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float32), g)
+    plan_env["PW4_PREFILL_EXACT"] = exact
+    plan_env["PW4_PREFILL_SPLITS"] = str(splits)
+    ys = {}
+    for rows in (128, 256):
+        plan_env["PW4_PREFILL_ROWS"] = str(rows)
+        ys[rows] = ops.gemm_w4a16_marlin(c.x, wm, sm, g)
+    check(ys[128], c.y_ref, dtype, f"128-row tiles {dtype} exact={exact}")
+    assert torch.equal(ys[256], ys[128]), (ys[256].float() - ys[128].float()).abs().max().item()
