@@ -32,6 +32,8 @@ Also reported:
   prefill       = M in {256, 1024, 4096} over the same layers (BASELINE
                   configs[2]), TFLOP/s = 2*M*N*K / mean launch time, vs
                   2516.6 TFLOP/s fp16 MFMA;
+  prefill_bf16  = the same with bf16 activations (the reference engine's
+                  dtype; 2516.6 TFLOP/s bf16 MFMA);
   stack         = the 32-layer Llama-3-8B linear stack (q, k, v, o, gate, up,
                   down per layer) replayed as one HIP graph
                   per step at M = 1 and M = 32: linear-layer time per decode
@@ -43,6 +45,9 @@ Also reported:
                   host's cores over bounded samples of every config;
   roofline.copy_ceiling / read_ceiling = a 512 MiB device copy and 1 GiB
                   read-only reductions: what HBM gives a simple stream;
+  roofline.read_floor = per layer, a plain streaming read of the layer's
+                  decode bytes (the kernel's own duration): frac_of_read_floor
+                  is that time over the decode kernel's, per shape and mean;
   prefill_dense_fp16_yardstick = the dense fp16 library GEMM (hipBLASLt
                   through torch) at the M = 4096 shapes;
   repack        = repack_w4a16 per layer, GB/s of words and scales moved.
@@ -575,6 +580,52 @@ def measure_read_ceiling(torch, dev) -> dict:
                     "read; the best grid of the probe"}
 
 
+def measure_read_floor(torch, dev) -> dict:
+    """Per Llama-3-8B layer: how long a plain streaming read of that layer's decode bytes
+    (weights, scales, x and y at M = 1) takes -- the probe kernel's own duration, from HIP
+    events that hipExtLaunchKernel fills with the dispatch's start and end, as for the
+    decode kernel.  Each launch reads the next slice of a 1 GiB buffer (a slice recurs only
+    after 1 GiB of other reads, so it comes from HBM, not the 256 MB MALL); 40 launches at
+    1, 2 and 4 workgroups of 256 per CU, the best grid's mean reported."""
+    import ctypes
+
+    import pulsar_amd
+
+    probe = ctypes.CDLL(os.path.join(os.path.dirname(pulsar_amd.__file__), "libpw4_probe.so"))
+    probe.pw4_probe_stream_read_timed.restype = ctypes.c_int
+    probe.pw4_probe_stream_read_timed.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32,
+                                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                  ctypes.c_void_p]
+    t = torch.ones(READ_BYTES // 4, dtype=torch.int32, device=dev)
+    sink = torch.zeros(1024, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    reps = 40
+    out = {}
+    for name, k, n in LLAMA8B:
+        nb = decode_bytes(1, k, n) // 256 * 256
+        slots = READ_BYTES // nb
+        best = None
+        for wpc in (1, 2, 4):
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for a, b in ev:  # create the events before handing them over
+                a.record(stream)
+                b.record(stream)
+            for r in range(reps):
+                rc = probe.pw4_probe_stream_read_timed(t.data_ptr() + (r % slots) * nb, nb, wpc * cus, 0xDEADBEEF,
+                                                       sink.data_ptr(), stream.cuda_stream, ev[r][0], ev[r][1])
+                if rc != 0:
+                    raise RuntimeError(f"pw4_probe_stream_read_timed failed: hipError {rc}")
+            stream.synchronize()
+            us = sum(a.elapsed_time(b) for a, b in ev) / reps * 1e3
+            if best is None or us < best[0]:
+                best = (us, wpc)
+        out[name] = {"bytes": nb, "us": round(best[0], 2), "GB/s": round(nb / (best[0] * 1e-6) / 1e9, 1),
+                     "workgroups_per_cu": best[1]}
+    del t, sink
+    return out
+
+
 def repack_bench(torch, dev) -> dict:
     """repack_w4a16 (the reference's one-time CT -> MARLIN repack) per Llama-3-8B layer:
     HIP events around each call on two copies in turn, median of 5.  Bytes: the CT words
@@ -775,9 +826,10 @@ def main() -> int:
     # achievable-HBM context: a 512 MiB device-to-device copy (read + write bytes), and
     # read-only streams of 1 GiB (torch reductions: the weights of a decode GEMM are read,
     # never written)
-    copy_ceiling = read_ceiling = None
+    copy_ceiling = read_ceiling = read_floor = None
     if not args.no_decode:
         read_ceiling = measure_read_ceiling(torch, dev)
+        read_floor = measure_read_floor(torch, dev)
         src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device=dev)
         dst = torch.empty_like(src)
         dst.copy_(src)
@@ -791,6 +843,11 @@ def main() -> int:
         copy_ceiling = {"GB/s": round(2 * COPY_BYTES / (ms * 1e-3) / 1e9, 1), "bytes_moved": 2 * COPY_BYTES,
                         "what": "torch copy_ of 512 MiB fp16 on the device, median of 5, read + write bytes"}
         del src, dst
+    floor_frac = None
+    if read_floor is not None and per_gemm and all("kernel_us" in v for v in per_gemm.values()):
+        ratios = {key: read_floor[key.rsplit("_m", 1)[0]]["us"] / v["kernel_us"] for key, v in per_gemm.items()}
+        floor_frac = {"mean": round(sum(ratios.values()) / len(ratios), 3),
+                      "per_shape": {key: round(r, 3) for key, r in ratios.items()}}
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "decode_traffic.json")
@@ -800,12 +857,11 @@ def main() -> int:
         except (OSError, ValueError):
             traffic = None
 
-    prefill = None
-    if not args.no_prefill:
-        prefill = {}
+    def prefill_sweep(xdtype):
+        out = {}
         for pm in PREFILL_M:
             for name, k, n in LLAMA8B:
-                x = torch.randn(pm, k, device=dev).half()
+                x = torch.randn(pm, k, device=dev).to(xdtype)
                 w = weights[name][0]
                 for _ in range(2):
                     gemm_fp16_scales(x, w)
@@ -819,9 +875,16 @@ def main() -> int:
                 torch.cuda.synchronize()
                 ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
                 tf = 2.0 * pm * n * k / (ms * 1e-3) / 1e12
-                prefill[f"{name}_m{pm}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
-                                            "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3)}
+                out[f"{name}_m{pm}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+                                        "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3)}
                 del x
+        return out
+
+    prefill = prefill_bf16 = None
+    if not args.no_prefill:
+        prefill = prefill_sweep(torch.float16)
+        # bf16 activations (the reference engine's dtype), same weights and fp16 scales
+        prefill_bf16 = prefill_sweep(torch.bfloat16)
     repack = None if args.no_prefill else repack_bench(torch, dev)
     dense = None if args.no_prefill else dense_yardstick(torch, dev, args.prefill_reps)
     del weights, xs
@@ -882,10 +945,14 @@ def main() -> int:
             "read_ceiling": read_ceiling,
             "frac_of_read_ceiling": None if achieved is None or read_ceiling is None else
             round(achieved / read_ceiling["GB/s"], 4),
+            "read_floor": read_floor,
+            # per shape: the layer's streaming-read time over the decode kernel's own time
+            "frac_of_read_floor": floor_frac,
         },
         "decode": per_gemm,
         "reference_api": ref_api,
         "prefill": prefill,
+        "prefill_bf16": prefill_bf16,
         "prefill_dense_fp16_yardstick": dense,
         "repack": repack,
         "stack": stack,

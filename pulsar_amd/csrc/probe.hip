@@ -6,6 +6,7 @@
 // flight per iteration, and folds them into an XOR; the fold is stored only if
 // it equals a value the caller never passes (`sink` is written by no launch in
 // practice), so the loads stay but nothing is written.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -43,6 +44,20 @@ int pw4_probe_stream_read(const void* p, int64_t bytes, int blocks, uint32_t nev
     }
     hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
                        reinterpret_cast<const u32x4*>(p), bytes / 16, never, sink);
+    return (int)hipGetLastError();
+}
+
+// The same read, launched through hipExtLaunchKernel with two HIP events that
+// take the dispatch's own start and end timestamps (the kernel's duration
+// without the queue latency in front of it).
+int pw4_probe_stream_read_timed(const void* p, int64_t bytes, int blocks, uint32_t never, uint32_t* sink,
+                                hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+    if (p == nullptr || sink == nullptr || bytes <= 0 || bytes % 16 != 0 || blocks <= 0 ||
+        (reinterpret_cast<uintptr_t>(p) & 15) != 0 || start == nullptr || stop == nullptr) {
+        return (int)hipErrorInvalidValue;
+    }
+    hipExtLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, start, stop, 0,
+                          reinterpret_cast<const u32x4*>(p), bytes / 16, never, sink);
     return (int)hipGetLastError();
 }
 

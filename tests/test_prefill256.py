@@ -40,8 +40,10 @@ def test_prefill_marlin_ragged(tile, m, n, k, g):
     check(y, c.y_ref, torch.float16, f"tile={tile} m={m} n={n} k={k} g={g}")
 
 
-@pytest.mark.parametrize("num_splits", [1, 2, 3, 7])
+@pytest.mark.parametrize("num_splits", [1, 2, 3, 7, 8, 11])
 def test_prefill_marlin_split(tile, num_splits):
+    """Forced K slices, fewer and more than the 8 the automatic plans use; fp32 partials
+    summed in slice order by the combine pass."""
     m, n, k, g = 600, 384, 2048, 128
     c = reference_case(m, n, k, g, torch.float16, seed=12)
     wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float16), g)
@@ -187,3 +189,24 @@ def test_prefill_tile_shapes_bit_identical(plan_env, dtype, exact, splits):
         ys[rows] = ops.gemm_w4a16_marlin(c.x, wm, sm, g)
     check(ys[128], c.y_ref, dtype, f"128-row tiles {dtype} exact={exact}")
     assert torch.equal(ys[256], ys[128]), (ys[256].float() - ys[128].float()).abs().max().item()
+
+
+@pytest.mark.parametrize("rows", [128, 256])
+def test_prefill_split_sum_repeated_calls(plan_env, rows):
+    """K-slice plans of different tile and slice counts in a row on one stream, sharing the
+    shim's workspace, then the first again: each matches the oracle, and the repeated call is
+    bit-identical to the first (the fixed-order sum does not depend on what ran before)."""
+    plan_env["PW4_PREFILL_ROWS"] = str(rows)
+    g = 128
+    cases = [(300, 520, 1024, 4), (700, 1032, 2048, 8), (129, 264, 1024, 2), (300, 520, 1024, 4)]
+    first = None
+    for i, (m, n, k, s) in enumerate(cases):
+        plan_env["PW4_PREFILL_SPLITS"] = str(s)
+        c = reference_case(m, n, k, g, torch.float16, seed=21 + (i % 3))
+        wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float16), g)
+        y = ops.gemm_w4a16_marlin(c.x, wm, sm, g)
+        check(y, c.y_ref, torch.float16, f"rows={rows} m={m} n={n} splits={s} call {i}")
+        if i == 0:
+            first = y.clone()
+        elif i == 3:
+            assert torch.equal(y, first)

@@ -107,6 +107,8 @@ CASES = [
     (300, 1024, 512, torch.float16, {"PW4_PREFILL_SPLITS": "1"}, True),    # 256-wide prefill, unsplit
     (200, 1024, 512, torch.bfloat16, {"PW4_PREFILL_SPLITS": "1"}, False),  # the same, bf16 x
     (129, 512, 2048, torch.float16, {"PW4_PREFILL_SPLITS": "4"}, True),    # 256-wide, K slices -> combine
+    (300, 1040, 1024, torch.bfloat16, {"PW4_PREFILL_SPLITS": "3", "PW4_PREFILL_ROWS": "256"}, False),  # 8 waves
+    (129, 512, 2048, torch.float16, {"PW4_PREFILL_SPLITS": "12"}, True),   # 256-wide, 12 slices
     (100, 512, 4096, torch.bfloat16, {"PW4_PREFILL_TILE": "128"}, False),  # 128 x 128 kernel, K slices
     (700, 1024, 256, torch.float16, {"PW4_PREFILL_TILE": "128"}, False),   # 128 x 128 kernel, unsplit
 ]
