@@ -574,8 +574,9 @@ READ_BYTES = 1 << 30
 
 def measure_read_ceiling(torch, dev) -> dict:
     """HBM read-only rate over 1 GiB (four times the MALL): the streaming-read probe
-    (pulsar_amd/libpw4_probe.so, 16-byte loads, grid-stride) at a few grid sizes, median of
-    5 each, the best reported; torch reductions over the same buffer alongside."""
+    (pulsar_amd/libpw4_probe.so, 16-byte loads, grid-stride, plain or non-temporal) at a
+    few grid sizes, median of 5 each, the best reported; torch reductions over the same
+    buffer alongside."""
     import ctypes
 
     import pulsar_amd
@@ -596,23 +597,24 @@ def measure_read_ceiling(torch, dev) -> dict:
 
     probe = ctypes.CDLL(os.path.join(os.path.dirname(pulsar_amd.__file__), "libpw4_probe.so"))
     probe.pw4_probe_stream_read.restype = ctypes.c_int
-    probe.pw4_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32,
-                                            ctypes.c_void_p, ctypes.c_void_p]
+    probe.pw4_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
     stream = torch.cuda.current_stream().cuda_stream
 
-    def read(blocks):
-        rc = probe.pw4_probe_stream_read(t.data_ptr(), READ_BYTES, blocks, 0xDEADBEEF, sink.data_ptr(), stream)
+    def read(blocks, nt):
+        rc = probe.pw4_probe_stream_read(t.data_ptr(), READ_BYTES, blocks, nt, 0xDEADBEEF, sink.data_ptr(), stream)
         if rc != 0:
             raise RuntimeError(f"pw4_probe_stream_read failed: hipError {rc}")
 
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    probe_rates = {f"probe_{w}x{cus}_wg": rate(lambda w=w: read(w * cus)) for w in (1, 2, 4, 8, 16)}
+    probe_rates = {f"probe_{w}x{cus}_wg{'_nt' if nt else ''}": rate(lambda w=w, nt=nt: read(w * cus, nt))
+                   for w in (1, 2, 4, 8, 16) for nt in (0, 1)}
     torch_rates = {"torch_amax_int32": rate(lambda: t.amax()), "torch_sum_f32": rate(lambda: t.view(torch.float32).sum())}
     del t, sink
     best = max(probe_rates, key=probe_rates.get)
     return {"GB/s": probe_rates[best], "op": best, "all": {**probe_rates, **torch_rates}, "bytes_read": READ_BYTES,
-            "what": "streaming read of 1 GiB (16-byte loads, grid-stride, workgroups of 256), median of 5, bytes "
-                    "read; the best grid of the probe"}
+            "what": "streaming read of 1 GiB (16-byte loads, plain or non-temporal, grid-stride, workgroups of "
+                    "256), median of 5, bytes read; the best grid and load kind of the probe"}
 
 
 def measure_read_floor(torch, dev) -> dict:
@@ -621,16 +623,17 @@ def measure_read_floor(torch, dev) -> dict:
     events that hipExtLaunchKernel fills with the dispatch's start and end, as for the
     decode kernel.  Each launch reads the next slice of a 1 GiB buffer (a slice recurs only
     after 1 GiB of other reads, so it comes from HBM, not the 256 MB MALL); 40 launches at
-    1, 2 and 4 workgroups of 256 per CU, the best grid's mean reported."""
+    1, 2 and 4 workgroups of 256 per CU, plain and non-temporal loads, the best one's mean
+    reported."""
     import ctypes
 
     import pulsar_amd
 
     probe = ctypes.CDLL(os.path.join(os.path.dirname(pulsar_amd.__file__), "libpw4_probe.so"))
     probe.pw4_probe_stream_read_timed.restype = ctypes.c_int
-    probe.pw4_probe_stream_read_timed.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32,
-                                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
-                                                  ctypes.c_void_p]
+    probe.pw4_probe_stream_read_timed.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                                  ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
+                                                  ctypes.c_void_p, ctypes.c_void_p]
     t = torch.ones(READ_BYTES // 4, dtype=torch.int32, device=dev)
     sink = torch.zeros(1024, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream()
@@ -642,21 +645,24 @@ def measure_read_floor(torch, dev) -> dict:
         slots = READ_BYTES // nb
         best = None
         for wpc in (1, 2, 4):
-            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-            for a, b in ev:  # create the events before handing them over
-                a.record(stream)
-                b.record(stream)
-            for r in range(reps):
-                rc = probe.pw4_probe_stream_read_timed(t.data_ptr() + (r % slots) * nb, nb, wpc * cus, 0xDEADBEEF,
-                                                       sink.data_ptr(), stream.cuda_stream, ev[r][0], ev[r][1])
-                if rc != 0:
-                    raise RuntimeError(f"pw4_probe_stream_read_timed failed: hipError {rc}")
-            stream.synchronize()
-            us = sum(a.elapsed_time(b) for a, b in ev) / reps * 1e3
-            if best is None or us < best[0]:
-                best = (us, wpc)
+            for nt in (0, 1):
+                ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                      for _ in range(reps)]
+                for a, b in ev:  # create the events before handing them over
+                    a.record(stream)
+                    b.record(stream)
+                for r in range(reps):
+                    rc = probe.pw4_probe_stream_read_timed(t.data_ptr() + (r % slots) * nb, nb, wpc * cus, nt,
+                                                           0xDEADBEEF, sink.data_ptr(), stream.cuda_stream, ev[r][0],
+                                                           ev[r][1])
+                    if rc != 0:
+                        raise RuntimeError(f"pw4_probe_stream_read_timed failed: hipError {rc}")
+                stream.synchronize()
+                us = sum(a.elapsed_time(b) for a, b in ev) / reps * 1e3
+                if best is None or us < best[0]:
+                    best = (us, wpc, nt)
         out[name] = {"bytes": nb, "us": round(best[0], 2), "GB/s": round(nb / (best[0] * 1e-6) / 1e9, 1),
-                     "workgroups_per_cu": best[1]}
+                     "workgroups_per_cu": best[1], "nontemporal": bool(best[2])}
     del t, sink
     return out
 
