@@ -168,7 +168,6 @@ __device__ __forceinline__ float half_to_f32(uint16_t v) {
 //   X     [M][rowstride] halves, rowstride = kps + 8, padded to whole 1 KB
 //         copy blocks: the workgroup's activation slice in natural K order
 //   RED   [2][8 waves][MT*16][16] fp32: per-unit cross-wave sums, double buffered
-//   CP,CQ [steps][NGRP][MT*16] fp32: bf16 only, per-step correction terms
 __host__ __device__ inline size_t x_slots(int M, int kps) { return ((size_t)M * (kps / 8 + 1) + 63) / 64 * 64; }
 __host__ __device__ inline size_t red_floats(int mt) { return (size_t)2 * kWaves * mt * 16 * 16; }
 
@@ -178,7 +177,6 @@ __host__ __device__ inline size_t red_floats(int mt) { return (size_t)2 * kWaves
 // memory operation, the weight ring included.  The memory clobber keeps the
 // compiler from moving LDS accesses across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-__host__ __device__ inline size_t corr_floats(int kps, int ngrp, int mt) { return (size_t)(kps / 128) * ngrp * mt * 16; }
 
 template <bool BF16, int LAYOUT, typename ST, int MT, int NGRP, bool ZP, int U, bool TREE>
 __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
@@ -222,8 +220,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     const int spu_pad = (spu + U - 1) / U * U;  // positions per unit, a whole number of ring blocks
 
     float* RED = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + x_slots(M, a.k_per_split) * 16);
-    float* CP = RED + (a.red_single ? red_floats(MT) / 2 : red_floats(MT));
-    float* CQ = CP + corr_floats(a.k_per_split, NGRP, MT);
     const ST* scales = reinterpret_cast<const ST*>(a.scales);
 
     // ---- the activation slice into LDS --------------------------------------
@@ -324,59 +320,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
         }
     }
     __syncthreads();
-    if constexpr (BF16) {
-        // per-step corrections, stored negated: -(128 P + z Q) with P = Q = sum(x).
-        // Each sum is (128 / NGRP) / 8 16-byte chunks.  With few sums (small M)
-        // a sum spreads over an aligned group of L lanes, the most that keep the
-        // pass to one round over the workgroup, and ends in a butterfly; with
-        // many, each thread reads its sum's chunks itself.  L is a compile-time
-        // choice so that every variant's loops unroll.
-        constexpr int kChunks = 16 / NGRP;
-        const int items = M * nsteps * NGRP;
-        auto corr_pass = [&](auto lanes) {
-            constexpr int L = decltype(lanes)::value, cpl = kChunks / L;
-            const int part = tid & (L - 1);
-            for (int base = 0; base < items; base += kThreads / L) {
-                const int i = base + tid / L;  // the same for the whole group
-                if (i < items) {
-                    const int m = i % M, sg = i / M, st = sg / NGRP, gi = sg - st * NGRP;
-                    const int k = st * 128 + gi * (128 / NGRP) + part * cpl * 8;
-                    float p = 0.f;
-#pragma unroll
-                    for (int ch = 0; ch < cpl; ++ch) {
-                        const u32x4 v = *reinterpret_cast<const u32x4*>(smem + m * rs + k + ch * 8);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            p += __builtin_bit_cast(float, v[e] << 16) + __builtin_bit_cast(float, v[e] & 0xffff0000u);
-                        }
-                    }
-#pragma unroll
-                    for (int off = L / 2; off > 0; off >>= 1) p += __shfl_xor(p, off);
-                    if (part == 0) {
-                        const int idx = (st * NGRP + gi) * MP + m;
-                        if constexpr (ZP) {
-                            CP[idx] = -128.f * p;
-                            CQ[idx] = -p;
-                        } else {
-                            CP[idx] = -136.f * p;
-                        }
-                    }
-                }
-            }
-        };
-        // lane groups of L <= kChunks lanes
-        if (items * kChunks <= kThreads) {
-            corr_pass(std::integral_constant<int, kChunks>{});
-        } else if (kChunks >= 4 && items * 4 <= kThreads) {
-            corr_pass(std::integral_constant<int, (kChunks >= 4 ? 4 : 1)>{});
-        } else if (kChunks >= 2 && items * 2 <= kThreads) {
-            corr_pass(std::integral_constant<int, (kChunks >= 2 ? 2 : 1)>{});
-        } else {
-            corr_pass(std::integral_constant<int, 1>{});
-        }
-        __syncthreads();
-    }
-
     // ---- main loop -----------------------------------------------------------
     f32x4 acc[MT];
 #pragma unroll
@@ -405,21 +348,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
         for (int gi = 0; gi < NGRP; ++gi)
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                if constexpr (BF16) {
-                    const int idx = (st * NGRP + gi) * MP + mt * 16 + 4 * h;
-                    const f32x4 cp = *reinterpret_cast<const f32x4*>(CP + idx);
-                    if constexpr (ZP) {
-                        const f32x4 cq = *reinterpret_cast<const f32x4*>(CQ + idx);
+            for (int mt = 0; mt < MT; ++mt) tmp[gi][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // bf16: B = 128 + u (exact), so each group's sum carries (128 + z) * sum(x)
+        // too; a second MFMA on the same activations with B = -(128 + z) in every
+        // K position (exact in bf16: 0xC300 | z) removes it in the accumulator.
+        u32x4 zneg[NGRP];
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) tmp[gi][mt][r] = cp[r] + (float)zl[gi] * cq[r];
-                    } else {
-                        tmp[gi][mt] = cp;
-                    }
-                } else {
-                    tmp[gi][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                }
-            }
+        for (int gi = 0; gi < NGRP; ++gi) {
+            const uint32_t v = (0xC300u | zl[gi]) * 0x10001u;
+            zneg[gi] = u32x4{v, v, v, v};
+        }
         uint32_t zlo = zl[0], zhi = zl[0];
 #pragma unroll
         for (int gi = 1; gi < NGRP; ++gi) {
@@ -465,6 +403,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
                         if ((s < 2 ? g_lo : g_hi) != gi) ag = u32x4{0u, 0u, 0u, 0u};
                     }
                     tmp[gi][mt] = mfma16x16x32<BF16>(ag, b, tmp[gi][mt]);
+                    if constexpr (BF16) tmp[gi][mt] = mfma16x16x32<BF16>(ag, zneg[gi], tmp[gi][mt]);
                 }
             }
         }
@@ -806,7 +745,6 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
 size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single) {
     const int mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     size_t b = x_slots(M, kps) * 16 + red_floats(mt) * 4 / (red_single ? 2 : 1);
-    if (bf16) b += corr_floats(kps, ngrp, mt) * 4 * (zp ? 2 : 1);
     return b;
 }
 
