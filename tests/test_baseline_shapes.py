@@ -37,6 +37,23 @@ def test_decode_llama8b(layer, m):
 
 
 @pytest.mark.parametrize("layer", list(LLAMA8B))
+@pytest.mark.parametrize("m", [1, 16, 256])
+def test_llama8b_bf16(layer, m):
+    """bf16 activations (the reference engine's dtype) at the Llama-3-8B shapes, decode and a
+    prefill size, at the reference's bf16 bar; prefill on a row subset."""
+    k, n = LLAMA8B[layer]
+    rows = None if m <= 16 else np.unique(np.concatenate([np.arange(0, m, 7), [m - 1]]))
+    c = baseline_case(m, n, k, 128, dtype=torch.bfloat16, seed=2, rows=rows)
+    wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float16), 128)
+    y = ops.gemm_w4a16_marlin(c.x, wm, sm, 128)
+    assert y.dtype == torch.bfloat16
+    if rows is not None:
+        y = y[torch.from_numpy(rows).cuda()]
+    r = check(y, c.y_ref, torch.bfloat16, f"bf16 {layer} m={m}")
+    print(f"bf16 {layer} m={m}: {r}")
+
+
+@pytest.mark.parametrize("layer", list(LLAMA8B))
 @pytest.mark.parametrize("m", [256, 1024, 4096])
 def test_prefill_llama8b_rows(layer, m):
     k, n = LLAMA8B[layer]
