@@ -10,6 +10,9 @@ produces, next to this file,
   libpw4_probe.so             a streaming-read probe that bench.py times for the
                               read-only HBM ceiling (measurement only; not part of
                               the library or its ABI)
+  pw4_selftest                a torch-free C++ program that calls the C ABI on
+                              hipMalloc'd memory and checks the results on the CPU
+                              (links libpulsar_w4a16.so and the HIP runtime only)
 """
 
 from __future__ import annotations
@@ -33,6 +36,8 @@ TORCH_LIB_NAME = "_pulsar_w4a16_torch.so"
 TORCH_SOURCES = ["torch_ops.cpp", "model.cpp"]
 PROBE_SOURCE = "probe.hip"
 PROBE_LIB_NAME = "libpw4_probe.so"
+SELFTEST_SOURCE = "capi_selftest.cpp"
+SELFTEST_NAME = "pw4_selftest"
 
 # gfx950 only.  Packed-fp32 instructions are disabled for the device pass; the
 # host pass prints a harmless "not a recognized feature" warning for it.
@@ -134,10 +139,25 @@ def build_probe(verbose: bool = False) -> str:
     return out
 
 
+def build_selftest(verbose: bool = False) -> str:
+    """Host-only C++ (g++): no torch and no device code of its own."""
+    out = os.path.join(HERE, SELFTEST_NAME)
+    tmp = out + ".tmp"
+    cmd = [
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__=1",
+        f"-I{ROCM}/include", f"-I{INCLUDE}", os.path.join(CSRC, SELFTEST_SOURCE), "-o", tmp,
+        f"-L{HERE}", "-lpulsar_w4a16", f"-L{ROCM}/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM}/lib",
+    ]
+    _run_parallel([cmd], verbose)
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False) -> None:
     build_hip(verbose)
     build_torch(verbose)
     build_probe(verbose)
+    build_selftest(verbose)
 
 
 if __name__ == "__main__":
