@@ -293,10 +293,16 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         while (nb > 16 && ncols % nb != 0) nb /= 2;
         const int64_t ncg = ceil_div(ncols, nb);
         // ring depth: a unit of at most 4 steps per wave needs no more (its
-        // steps pad to the ring depth)
+        // steps pad to the ring depth).  Up to M = 8 the 4-step ring also
+        // wins on long units: 8 waves x 4 x 1 KB is 32 KB of weight loads in
+        // flight per CU, where a streaming read peaks; 64 KB per CU queues
+        // behind itself (a copy of the kernel's load walk, no compute: down
+        // 6.5 us with 4 steps in flight against 7.2 with 8; the kernel: down
+        // M = 1 -8%, Llama-70B layers at M = 1 -3..-8%).  At M = 16 the
+        // deeper ring still covers the 16-row MFMA work (70B layers +2% at 4).
         const int64_t kwn = 8 / (nb / 16);
         const int64_t spu = std::max<int64_t>(ceil_div(ceil_div(kps, 128), kwn), 1);
-        dc.ring = spu <= 4 || dc.ngrp > 2 ? 4 : 8;
+        dc.ring = spu <= 4 || dc.ngrp > 2 || M <= 8 ? 4 : 8;
         // Persistent grid: one or two workgroups per CU (register and LDS
         // budget), then as few units per workgroup as possible with the
         // least per-CU load.
