@@ -62,9 +62,21 @@ constexpr size_t kCounterBytes = 65536;
 constexpr int64_t kMaxCounterCols = (int64_t)(kCounterBytes / sizeof(int32_t));
 constexpr size_t kSlotBytes = kZeroRegion - kCounterBytes;
 
+// Plan overrides for tuning sweeps and tests.  They are read from the
+// environment on every call only when PW4_PLAN_OVERRIDES=1 was set when the
+// process first planned a GEMM; otherwise no call reads the environment (six
+// lookups cost ~0.5 us of host time per call with a typical environment).
+const char* plan_env(const char* name) {
+    static const bool enabled = [] {
+        const char* e = std::getenv("PW4_PLAN_OVERRIDES");
+        return e != nullptr && e[0] == '1';
+    }();
+    return enabled ? std::getenv(name) : nullptr;
+}
+
 // Decode column width override (16, 32 or 64) for tuning sweeps; 0 = heuristic.
 int decode_nb_override() {
-    const char* e = std::getenv("PW4_DECODE_NB");
+    const char* e = plan_env("PW4_DECODE_NB");
     if (!e) return 0;
     const int v = std::atoi(e);
     return (v == 16 || v == 32 || v == 64) ? v : 0;
@@ -72,7 +84,7 @@ int decode_nb_override() {
 
 // Prefill tile override (128 or 256) for tuning sweeps; 0 = heuristic.
 int prefill_tile_override() {
-    const char* e = std::getenv("PW4_PREFILL_TILE");
+    const char* e = plan_env("PW4_PREFILL_TILE");
     if (!e) return 0;
     const int v = std::atoi(e);
     return (v == 128 || v == 256) ? v : 0;
@@ -81,13 +93,13 @@ int prefill_tile_override() {
 // Rows of the 256-wide prefill tiles (256 or 128) and the K-slice count of
 // an unforced prefill plan (1..64), for tuning sweeps; 0 = heuristic.
 int prefill_rows_override() {
-    const char* e = std::getenv("PW4_PREFILL_ROWS");
+    const char* e = plan_env("PW4_PREFILL_ROWS");
     if (!e) return 0;
     const int v = std::atoi(e);
     return (v == 128 || v == 256) ? v : 0;
 }
 int prefill_splits_override() {
-    const char* e = std::getenv("PW4_PREFILL_SPLITS");
+    const char* e = plan_env("PW4_PREFILL_SPLITS");
     if (!e) return 0;
     const int v = std::atoi(e);
     return (v >= 1 && v <= 64) ? v : 0;
@@ -96,7 +108,7 @@ int prefill_splits_override() {
 // Decode K-split override for tuning sweeps (2, 4 or 8: exchange-tree
 // slices even where the activations fit in LDS); 0 = heuristic.
 int decode_splits_override() {
-    const char* e = std::getenv("PW4_DECODE_SPLITS");
+    const char* e = plan_env("PW4_DECODE_SPLITS");
     if (!e) return 0;
     const int v = std::atoi(e);
     return (v == 2 || v == 4 || v == 8) ? v : 0;
@@ -123,9 +135,10 @@ struct Prefill256Plan {
 };
 
 // Exact scaling of the 256-wide prefill kernel with fp16 activations (see
-// gemm_prefill_256.hip): on unless PW4_PREFILL_EXACT=0 (A/B sweeps only).
+// gemm_prefill_256.hip): on unless overridden with PW4_PREFILL_EXACT=0 (A/B
+// sweeps only).
 bool prefill_exact_enabled() {
-    const char* e = std::getenv("PW4_PREFILL_EXACT");
+    const char* e = plan_env("PW4_PREFILL_EXACT");
     return !(e && e[0] == '0');
 }
 
@@ -323,7 +336,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
                 best_wps = wps;
             }
         }
-        if (const char* e = std::getenv("PW4_DECODE_WPS")) {  // tuning sweeps only
+        if (const char* e = plan_env("PW4_DECODE_WPS")) {  // tuning sweeps only
             const int64_t v = std::atoll(e);
             if (v >= 1 && v <= 4 * (int64_t)cus) best_wps = std::min<int64_t>(v, ncg);
         }

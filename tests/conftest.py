@@ -7,6 +7,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+# Some tests pin a plan (tile rows, K slices, exact scaling) through the
+# library's PW4_* plan overrides; the library reads them only when this is set
+# before its first GEMM call in the process.
+os.environ["PW4_PLAN_OVERRIDES"] = "1"
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")

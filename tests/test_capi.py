@@ -113,6 +113,27 @@ def test_workspace_queries(lib):
     assert ws_perm1 >= (16 << 20) + 512 * 2
 
 
+def test_plan_overrides_are_live(lib):
+    """The tests that pin a plan through PW4_* variables (tests/conftest.py
+    enables them for the process) would compare a plan with itself if the
+    library ignored them: an unforced prefill plan must follow
+    PW4_PREFILL_SPLITS, which the workspace query shows as its fp32 partials."""
+    M, N, K, G = 512, 4096, 4096, 128
+    old = os.environ.get("PW4_PREFILL_SPLITS")
+    try:
+        os.environ["PW4_PREFILL_SPLITS"] = "1"
+        unsplit = lib.pw4_gemm_w4a16_marlin_workspace_size(M, N, K, G, 0, 0)
+        os.environ["PW4_PREFILL_SPLITS"] = "3"
+        split3 = lib.pw4_gemm_w4a16_marlin_workspace_size(M, N, K, G, 0, 0)
+    finally:
+        if old is None:
+            os.environ.pop("PW4_PREFILL_SPLITS", None)
+        else:
+            os.environ["PW4_PREFILL_SPLITS"] = old
+    assert unsplit == 0
+    assert split3 >= 3 * M * N * 4
+
+
 def test_missing_workspace_is_rejected(lib):
     dummy = ctypes.c_void_p(16)
     assert lib.pw4_gemm_w4a16(dummy, 0, dummy, dummy, dummy, 4, 256, 512, 64, 3, None, 0, None) == -3
