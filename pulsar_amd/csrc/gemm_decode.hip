@@ -13,8 +13,8 @@
 // (c = l%16, h = l/16) fetches the four words of column c in 32-K tile h,
 // which are 16 contiguous bytes in both layouts (MARLIN: a wave instruction
 // reads four fully used 256-byte segments).  The loads of the wave's next U
-// steps sit in a register ring that runs on across unit boundaries, so a unit
-// change costs no HBM round trip.  The activation slice is copied into LDS
+// steps (4, or 8 for long units at M > 8) sit in a register ring that runs on
+// across unit boundaries, so a unit change costs no HBM round trip.  The activation slice is copied into LDS
 // once per workgroup with global_load_lds (no VGPRs), issued before the first
 // weight loads.
 //
@@ -22,17 +22,23 @@
 // exactly (exponent splice of the nibble into 1024.0, then one packed add or
 // fma per pair), accumulated per 128-K step in fp32 and scaled per column in
 // fp32, so q * scale is never rounded to 16 bits.  bf16 has no cheap packed
-// subtract, so B = 128 + u (exact) and each step's accumulators start from
-// -(128 + z) * sum(x) of the step, summed from the staged slice.  The
+// subtract, so B = 128 + u (exact), and a second MFMA on the same activation
+// fragment with B = -(128 + z) in every K position (exact in bf16) takes the
+// bias back out of the fp32 accumulator.  The
 // activations stay in natural K order: MARLIN word tg of a 32-K tile holds
 // K {8p + 2tg, 8p + 2tg + 1} in its nibble pair p, so pair s of the tile's
 // four words is the contiguous run [8s, 8s + 8) that MFMA s multiplies; a
 // compressed-tensors word is such a run already (its pairs re-ordered with
 // v_perm).  Either way the A operand is one 16-byte LDS read.
 //
-// K slices across workgroups.  Every workgroup writes its fp32 partial tile
-// and the last to arrive for a unit (arrival counter) sums the partials in
-// slice order -- the fixed-order combine of the reference
+// K slices across workgroups, when the activation slice does not fit in LDS.
+// Exchange tree (TREE instantiations; power-of-two slice counts up to 8): the
+// slices of a unit pair up level by level, each side swapping its fp32 sum
+// with its partner's through a 64-bit {value, flag} slot, so the sum is the
+// fixed tree ((s0 + s1) + (s2 + s3)) + ... whatever the arrival order.
+// Counter path (forced split counts, M > 32): every workgroup writes its fp32
+// partial tile and the last to arrive for a unit (arrival counter) sums the
+// partials in slice order -- the fixed-order combine of the reference
 // (w4a16_common.cuh:94-120) without a second launch -- and resets the counter.
 //
 // Reference counterpart: w4a16_marlin_kernel / gemm_w4a16_kernel at BM = 16
