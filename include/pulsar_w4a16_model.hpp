@@ -3,10 +3,13 @@
 // for q, k, v, o, gate, up and down (pulsar-core/src/model/qwen3.cpp:82-84,
 // 114, 117-119), with W taken from the weights map by name (qwen3.cpp:48-70).
 // A W4A16Linear holds one such weight in the MARLIN layout and computes
-// y = x @ dequant(W)^T through the operator API of pulsar_w4a16_ops.hpp;
-// Qwen3LayerW4A16 holds one layer's linears fused the way the kernels want
-// them (q|k|v as one GEMM, gate|up as one SiLU-gated GEMM) and runs the linear
-// part of Qwen3Model::block around the caller's norm weights and attention.
+// y = x @ dequant(W)^T (+ bias) through the operator API of
+// pulsar_w4a16_ops.hpp; Qwen3LayerW4A16 holds one layer's linears fused the way
+// the kernels want them (q|k|v as one GEMM, gate|up as one SiLU-gated GEMM) and
+// runs the linear part of Qwen3Model::block around the caller's norm weights
+// and attention.  The same layer serves Qwen2Model::block
+// (pulsar-core/src/model/qwen2.cpp:72-93), whose q, k and v projections carry
+// a bias (at::linear(h, W, b), qwen2.cpp:78-80): the biases ride in the linears.
 #pragma once
 
 #include <ATen/ATen.h>
@@ -27,9 +30,12 @@ class W4A16Linear {
     // qzeros int32 [K/G, N/8] (GPTQ zero points, absent: symmetric); perm int32 [K]
     // (act-order, absent: natural order).  silu_gate: the weight is gate|up interleaved
     // by 8 columns and forward() returns silu(gate) * up, [.., N/2].
+    // bias: [N] in any float dtype, added to the GEMM output: one rounding to x's
+    // dtype of the fp32 sum of the rounded GEMM output and the bias as stored.
     W4A16Linear(at::Tensor weight_marlin, at::Tensor scales, int64_t group_size, int64_t in_features,
                 int64_t out_features, std::optional<at::Tensor> qzeros = std::nullopt,
-                std::optional<at::Tensor> perm = std::nullopt, bool silu_gate = false);
+                std::optional<at::Tensor> perm = std::nullopt, bool silu_gate = false,
+                std::optional<at::Tensor> bias = std::nullopt);
 
     // The reference's quantized weight: weight_packed int32 [N, K/8] (two's complement
     // nibbles along K, ops.hpp:148-152) and weight_scale [N, K/G], repacked once with
@@ -44,9 +50,12 @@ class W4A16Linear {
     // N-concatenation of linears that share their input (q|k|v): the MARLIN words are
     // column-block major, so members whose N is a multiple of 64 concatenate as buffers.
     static W4A16Linear concat(const std::vector<W4A16Linear>& parts);
+    // The same linear with a bias [N] (or none).
+    W4A16Linear with_bias(std::optional<at::Tensor> bias) const;
     // Whether concat (or silu_gate, for two members) accepts these members: same K,
-    // group size, scale dtype, zero-point presence and act-order permutation, and
-    // N % 64 == 0 for every member but the last (every member for a SiLU gate).
+    // group size, scale dtype, zero-point presence, bias presence and act-order
+    // permutation, and N % 64 == 0 for every member but the last (every member for a
+    // SiLU gate, which takes no bias).
     static bool can_fuse(const std::vector<W4A16Linear>& parts, bool silu_gate = false);
     // The MLP gate silu(x Wg^T) * (x Wu^T) as one GEMM: gate and up interleaved by 8
     // columns, regrouped from the two repacked weights (no requantisation).
@@ -63,10 +72,11 @@ class W4A16Linear {
     const at::Tensor& scales() const { return scales_; }
     const std::optional<at::Tensor>& qzeros() const { return qzeros_; }
     const std::optional<at::Tensor>& perm() const { return perm_; }
+    const std::optional<at::Tensor>& bias() const { return bias_; }
 
    private:
     at::Tensor weight_marlin_, scales_;
-    std::optional<at::Tensor> qzeros_, perm_;
+    std::optional<at::Tensor> qzeros_, perm_, bias_;
     int64_t group_size_ = 0, in_ = 0, out_ = 0;
     bool silu_ = false;
 };
@@ -85,7 +95,8 @@ struct Qwen3LayerW4A16 {
     // The layer's quantized linears from a checkpoint's weights map, under the
     // engine's names (qwen3.cpp:55-69): <prefix>self_attn.{q,k,v,o}_proj.* and
     // <prefix>mlp.{gate,up,down}_proj.*, each either the reference's packed format
-    // (weight_packed, weight_scale) or GPTQ (qweight, scales, qzeros, g_idx).
+    // (weight_packed, weight_scale) or GPTQ (qweight, scales, qzeros, g_idx), plus
+    // an optional <...>_proj.bias (Qwen2's q, k and v, qwen2.cpp:57-62).
     static Qwen3LayerW4A16 from_weights(const c10::Dict<std::string, at::Tensor>& weights, const std::string& prefix,
                                         int64_t group_size);
 
@@ -112,5 +123,13 @@ using AttentionFn = std::function<at::Tensor(const at::Tensor& q, const at::Tens
 //   x = x + o_proj(o); h2 = rmsnorm(x, ln2); x = x + down(silu(gate(h2)) * up(h2))
 at::Tensor qwen3_block_w4a16(const Qwen3LayerW4A16& layer, const at::Tensor& x, const at::Tensor& ln1,
                              const at::Tensor& ln2, double eps, const AttentionFn& attention);
+
+// Qwen2Model::block (qwen2.cpp:72-93) has the same linear structure; its q, k and v
+// biases come with the layer (from_weights), and its RoPE (no QK-norm) is the
+// caller's, inside `attention`.
+inline at::Tensor qwen2_block_w4a16(const Qwen3LayerW4A16& layer, const at::Tensor& x, const at::Tensor& ln1,
+                                    const at::Tensor& ln2, double eps, const AttentionFn& attention) {
+    return qwen3_block_w4a16(layer, x, ln1, ln2, eps, attention);
+}
 
 }  // namespace pulsar

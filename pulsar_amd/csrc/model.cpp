@@ -39,26 +39,30 @@ std::optional<at::Tensor> maybe(const c10::Dict<std::string, at::Tensor>& w, con
     return w.at(name);
 }
 
-// One quantized linear under <p>: the reference's packed format or GPTQ.
+// One quantized linear under <p>: the reference's packed format or GPTQ, with
+// its bias when the map holds one (Qwen2's q, k and v).
 W4A16Linear load_linear(const c10::Dict<std::string, at::Tensor>& w, const std::string& p, int64_t group_size) {
     if (w.contains(p + "weight_packed")) {
-        return W4A16Linear::from_packed(w.at(p + "weight_packed"), need(w, p + "weight_scale"), group_size);
+        return W4A16Linear::from_packed(w.at(p + "weight_packed"), need(w, p + "weight_scale"), group_size)
+            .with_bias(maybe(w, p + "bias"));
     }
     TORCH_CHECK(w.contains(p + "qweight"), "Qwen3LayerW4A16: no quantized weight under '", p,
                 "' (expected weight_packed + weight_scale, or qweight + scales)");
     return W4A16Linear::from_gptq(w.at(p + "qweight"), need(w, p + "scales"), group_size, maybe(w, p + "qzeros"),
-                                  maybe(w, p + "g_idx"));
+                                  maybe(w, p + "g_idx"))
+        .with_bias(maybe(w, p + "bias"));
 }
 
 }  // namespace
 
 W4A16Linear::W4A16Linear(at::Tensor weight_marlin, at::Tensor scales, int64_t group_size, int64_t in_features,
                          int64_t out_features, std::optional<at::Tensor> qzeros, std::optional<at::Tensor> perm,
-                         bool silu_gate)
+                         bool silu_gate, std::optional<at::Tensor> bias)
     : weight_marlin_(std::move(weight_marlin)),
       scales_(std::move(scales)),
       qzeros_(has(qzeros) ? std::move(qzeros) : std::nullopt),
       perm_(has(perm) ? std::move(perm) : std::nullopt),
+      bias_(has(bias) ? std::move(bias) : std::nullopt),
       group_size_(group_size),
       in_(in_features),
       out_(out_features),
@@ -79,6 +83,16 @@ W4A16Linear::W4A16Linear(at::Tensor weight_marlin, at::Tensor scales, int64_t gr
     }
     if (perm_) TORCH_CHECK(perm_->dim() == 1 && perm_->size(0) == k, "W4A16Linear: perm must be int32 [K]");
     if (silu_) TORCH_CHECK(n % 16 == 0, "W4A16Linear: a SiLU gate needs N (gate|up) % 16 == 0");
+    if (bias_) {
+        TORCH_CHECK(!silu_, "W4A16Linear: a SiLU gate takes no bias");
+        TORCH_CHECK(bias_->dim() == 1 && bias_->size(0) == n && at::isFloatingType(bias_->scalar_type()),
+                    "W4A16Linear: bias must be a floating-point [N] = [", n, "]");
+        bias_ = bias_->contiguous();
+    }
+}
+
+W4A16Linear W4A16Linear::with_bias(std::optional<at::Tensor> bias) const {
+    return W4A16Linear(weight_marlin_, scales_, group_size_, in_, out_, qzeros_, perm_, silu_, std::move(bias));
 }
 
 W4A16Linear W4A16Linear::from_packed(const at::Tensor& weight_packed, const at::Tensor& weight_scale,
@@ -114,6 +128,7 @@ bool W4A16Linear::can_fuse(const std::vector<W4A16Linear>& parts, bool silu_gate
         const W4A16Linear& p = parts[i];
         if (p.silu_ || p.in_ != p0.in_ || p.group_size_ != p0.group_size_ ||
             p.scales_.scalar_type() != p0.scales_.scalar_type() || p.qzeros_.has_value() != p0.qzeros_.has_value() ||
+            p.bias_.has_value() != p0.bias_.has_value() || (silu_gate && p.bias_) ||
             p.perm_.has_value() != p0.perm_.has_value() || (p.perm_ && !at::equal(*p.perm_, *p0.perm_))) {
             return false;
         }
@@ -127,7 +142,7 @@ W4A16Linear W4A16Linear::concat(const std::vector<W4A16Linear>& parts) {
     TORCH_CHECK(!parts.empty(), "W4A16Linear::concat: no parts");
     if (parts.size() == 1) return parts[0];
     const W4A16Linear& p0 = parts[0];
-    std::vector<at::Tensor> words, scales, zeros;
+    std::vector<at::Tensor> words, scales, zeros, biases;
     int64_t n = 0;
     for (size_t i = 0; i < parts.size(); ++i) {
         const W4A16Linear& p = parts[i];
@@ -136,6 +151,7 @@ W4A16Linear W4A16Linear::concat(const std::vector<W4A16Linear>& parts) {
                         p.scales_.scalar_type() == p0.scales_.scalar_type(),
                     "W4A16Linear::concat: members differ in K, group size or scale dtype");
         TORCH_CHECK(p.qzeros_.has_value() == p0.qzeros_.has_value(), "W4A16Linear::concat: members differ in zero points");
+        TORCH_CHECK(p.bias_.has_value() == p0.bias_.has_value(), "W4A16Linear::concat: members differ in bias");
         TORCH_CHECK(p.perm_.has_value() == p0.perm_.has_value() && (!p.perm_ || at::equal(*p.perm_, *p0.perm_)),
                     "W4A16Linear::concat: members have different act-order permutations");
         TORCH_CHECK(i + 1 == parts.size() || p.out_ % kMarlinBN == 0,
@@ -143,10 +159,13 @@ W4A16Linear W4A16Linear::concat(const std::vector<W4A16Linear>& parts) {
         words.push_back(p.weight_marlin_);
         scales.push_back(p.scales_);
         if (p.qzeros_) zeros.push_back(*p.qzeros_);
+        if (p.bias_) biases.push_back(*p.bias_);
         n += p.out_;
     }
     return W4A16Linear(at::cat(words), at::cat(scales, 1), p0.group_size_, p0.in_, n,
-                       zeros.empty() ? std::nullopt : std::optional<at::Tensor>(at::cat(zeros, 1)), p0.perm_);
+                       zeros.empty() ? std::nullopt : std::optional<at::Tensor>(at::cat(zeros, 1)), p0.perm_,
+                       /*silu_gate=*/false,
+                       biases.empty() ? std::nullopt : std::optional<at::Tensor>(at::cat(biases)));
 }
 
 W4A16Linear W4A16Linear::silu_gate(const W4A16Linear& gate, const W4A16Linear& up) {
@@ -156,6 +175,7 @@ W4A16Linear W4A16Linear::silu_gate(const W4A16Linear& gate, const W4A16Linear& u
                 "W4A16Linear::silu_gate: gate and up differ in shape, group size or scale dtype");
     TORCH_CHECK(f % kMarlinBN == 0, "W4A16Linear::silu_gate: the intermediate size must be a multiple of 64");
     TORCH_CHECK(gate.qzeros_.has_value() == up.qzeros_.has_value(), "W4A16Linear::silu_gate: zero points must match");
+    TORCH_CHECK(!gate.bias_ && !up.bias_, "W4A16Linear::silu_gate: gate and up take no bias");
     TORCH_CHECK(gate.perm_.has_value() == up.perm_.has_value() && (!gate.perm_ || at::equal(*gate.perm_, *up.perm_)),
                 "W4A16Linear::silu_gate: gate and up have different act-order permutations");
     const int64_t nch = ceil_div(k, kMarlinBK), kg = k / g;
@@ -173,6 +193,9 @@ at::Tensor W4A16Linear::forward(const at::Tensor& x) const {
     auto x2 = x.reshape({-1, in_}).contiguous();
     at::Tensor y = silu_ ? gemm_w4a16_silu_mul_cuda(x2, weight_marlin_, scales_, qzeros_, perm_, group_size_)
                          : gemm_w4a16_gptq_cuda(x2, weight_marlin_, scales_, qzeros_, perm_, group_size_);
+    // at::linear's bias (qwen2.cpp:78-80): add_ sums the rounded GEMM output and the
+    // bias as stored in fp32 and rounds once to x's dtype
+    if (bias_) y.add_(*bias_);
     lead.push_back(out_features());
     return y.view(lead);
 }
