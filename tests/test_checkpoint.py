@@ -245,3 +245,24 @@ def test_fusion_skipped_when_members_differ(tmp_path):
     assert "model.layers.0.mlp.gate_up_proj.weight" in w
     _check_linears({k: v for k, v in w.items()}, {p: d for p, d in dense_w.items() if "layers.0.self_attn" in p
                                                   and "o_proj" not in p}, 3, seed=14)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bdtype", [torch.float32, torch.float16])
+def test_linear_bias(bdtype):
+    """W4A16Linear with a bias, as Qwen2's q, k and v projections carry one
+    (at::linear(h, W, b), pulsar-core/src/model/qwen2.cpp:78-80): the rounded
+    GEMM output plus the bias, rounded once, against the fp32 oracle plus bias."""
+    m, n, k, g = 5, 320, 1024, 128
+    p = O.make_problem(m, n, k, g, seed=11)
+    rng = np.random.default_rng(11)
+    b = (0.5 * rng.standard_normal(n)).astype(np.float32)
+    if bdtype == torch.float16:
+        b = b.astype(np.float16).astype(np.float32)
+    lin = W4A16Linear.from_packed(torch.from_numpy(p.ct_packed()).cuda(),
+                                  torch.from_numpy(p.scale_nk).cuda(), g,
+                                  bias=torch.from_numpy(b).to(bdtype).cuda())
+    x = torch.from_numpy(p.x16.view(np.float16)).cuda()
+    y = lin(x)
+    assert y.shape == (m, n) and y.dtype == torch.float16
+    check(y, O.gemm_f32(p.xf, p.dequant()) + b, torch.float16, f"bias {bdtype}")
