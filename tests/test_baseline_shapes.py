@@ -80,6 +80,24 @@ def test_act_order_llama70b(layer, m):
     print(f"act-order 70B {layer} m={m}: {r}")
 
 
+@pytest.mark.parametrize("layer", ["qkv", "down"])
+@pytest.mark.parametrize("m", [1, 16, 2048])
+def test_act_order_llama70b_bf16(layer, m):
+    """Config 4 with bf16 activations (the reference engine's dtype): asymmetric int4,
+    act-order, fp16 scales, at the reference's bf16 bar; M = 2048 on a row subset."""
+    k, n = LLAMA70B[layer]
+    rows = None if m <= 16 else np.arange(0, m, 97)
+    c = baseline_case(m, n, k, 128, dtype=torch.bfloat16, seed=5, symmetric=False, act_order=True, rows=rows)
+    wm, perm = ops.repack_w4a16_gptq(c.qweight(), torch.from_numpy(c.g_idx).cuda(), 128)
+    scales = torch.from_numpy(np.ascontiguousarray(c.scale_nk.T)).half().cuda()
+    y = ops.gemm_w4a16_gptq(c.x, wm, scales, c.qzeros(), perm, 128)
+    assert y.dtype == torch.bfloat16
+    if rows is not None:
+        y = y[torch.from_numpy(rows).cuda()]
+    r = check(y, c.y_ref, torch.bfloat16, f"act-order bf16 {layer} m={m}")
+    print(f"act-order 70B bf16 {layer} m={m}: {r}")
+
+
 @pytest.mark.parametrize("layer", ["o", "gate_up", "down"])
 def test_output_checksum_prefill(layer):
     """Column sums of y over ALL rows against the oracle: sum_m y[m, :] equals
