@@ -31,6 +31,8 @@ layer's copies in turn, so every launch reads its weights from HBM.
 Also reported:
   reference_api = the same sweep through the reference's API
                   (gemm_w4a16_marlin with fp32 scale_marlin from repack_w4a16);
+  decode_bf16   = the same sweep with bf16 activations (the reference
+                  engine's dtype): step-graph value and kernel durations;
   prefill       = M in {256, 1024, 4096} over the same layers (BASELINE
                   configs[2]), TFLOP/s = 2*M*N*K / mean launch time, vs
                   2516.6 TFLOP/s fp16 MFMA;
@@ -768,6 +770,7 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-reference-api", action="store_true")
+    ap.add_argument("--no-decode-bf16", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=10)
     ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--no-act-order", action="store_true", help="skip the 70B act-order layers (configs[3])")
@@ -870,6 +873,25 @@ def main() -> int:
         ref_api = {"value": round(tot_bytes / wall2 / 1e9, 2), "unit": "GB/s",
                    "per_gemm_us": {f"{name}_m{m}": round(ms * 1e3, 2) for (m, name, _, _), ms in zip(shapes, per2)}}
         del g2
+
+    # the same sweep with bf16 activations (the reference engine's dtype): step-graph
+    # value and the kernel's own duration per shape
+    dec_bf16 = None
+    if not args.no_decode and not args.no_decode_bf16:
+        xb = {key: t.to(torch.bfloat16) for key, t in xs.items()}
+        sgb = build_step_graph(torch, shapes, weights, xb, gemm_fp16_scales, stream)
+        wallb = time_step_graph(torch, sgb[0], args.steps, args.warmup, stream)
+        del sgb
+        own_b, call_b = time_each_launch(torch, shapes, weights, xb, gemm_fp16_scales, stream, args.steps * REPS)
+        own_b = [c if o is None else o for o, c in zip(own_b, call_b)]
+        ach_b = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) / (sum(own_b) * 1e-3) / 1e9
+        dec_bf16 = {"value": round(tot_bytes / wallb / 1e9, 2), "unit": "GB/s",
+                    "achieved": round(ach_b, 1), "frac": round(ach_b / HBM_PEAK_GBS, 4),
+                    "mean_launch_us": round(sum(own_b) / len(own_b) * 1e3, 3),
+                    "kernel_us": {f"{name}_m{m}": round(ms * 1e3, 2) for (m, name, _, _), ms in zip(shapes, own_b)},
+                    "what": "the decode sweep with bf16 x (same weights, fp16 scales): value over the step graph, "
+                            "achieved over the kernel's own mean duration, as the fp16 headline"}
+        del xb
 
     # achievable-HBM context: a 512 MiB device-to-device copy (read + write bytes), and
     # read-only streams of 1 GiB (torch reductions: the weights of a decode GEMM are read,
@@ -1001,6 +1023,7 @@ def main() -> int:
         },
         "decode": per_gemm,
         "reference_api": ref_api,
+        "decode_bf16": dec_bf16,
         "prefill": prefill,
         "prefill_bf16": prefill_bf16,
         "prefill_dense_fp16_yardstick": dense,
