@@ -390,9 +390,19 @@ def summarize_traffic(fetch_csv: str, write_csv: str) -> int:
     shapes = [(m, name, k, n) for m in DECODE_M for name, k, n in LLAMA8B]
     alg = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) / len(shapes)
     traffic = out["fetch"]["decode_mean_bytes_calibrated"] + out["write"]["decode_mean_bytes_calibrated"]
+    # the workload issues the shapes in sweep order, REPS launches each
+    per_shape = {}
+    dec = {label: [v for name, v in per_dispatch(path, counter) if "decode_kernel" in name]
+           for label, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE"))}
+    if all(len(v) == len(shapes) * REPS for v in dec.values()):
+        for i, (m, name, k, n) in enumerate(shapes):
+            b = sum(sum(dec[label][i * REPS:(i + 1) * REPS]) / REPS * 1024.0 * out[label]["calibration_factor"]
+                    for label in ("fetch", "write"))
+            per_shape[f"{name}_m{m}"] = {"bytes": round(b), "algorithmic": decode_bytes(m, k, n),
+                                         "ratio": round(b / decode_bytes(m, k, n), 4)}
     res = {"bytes_per_launch": round(traffic), "algorithmic_bytes_per_launch": round(alg),
            "traffic_over_algorithmic": round(traffic / alg, 4), "launches": "the 16 decode-sweep shapes x "
-           f"{REPS} launches each, fp16 scales", **out}
+           f"{REPS} launches each, fp16 scales", **out, "per_shape": per_shape}
     path = os.path.join(ROOT, "profiles", "decode_traffic.json")
     with open(path, "w") as f:
         json.dump(res, f, indent=1)

@@ -79,34 +79,6 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, c
 // the exact value 1024 + n; a nibble at bit 4 gives 1024 + 16n.  Each word
 // yields the pairs (n0,n4) (n1,n5) (n2,n6) (n3,n7).
 
-// fp16, integer exact: out = u - z for all eight nibbles.
-//   z1024 = (0x6400 | z) in both halves, z64 = (0x5400 | z << 4) in both halves.
-__device__ __forceinline__ u32x4 dq_f16_exact(uint32_t q, uint32_t z1024, uint32_t z64) {
-    const uint32_t q8 = q >> 8;
-    const f16x2 sixteenth = as_h2(0x2c002c00u);
-    u32x4 r;
-    r[0] = as_u32(as_h2((q & 0x000f000fu) | 0x64006400u) - as_h2(z1024));
-    r[1] = as_u32(as_h2((q & 0x00f000f0u) | 0x64006400u) * sixteenth - as_h2(z64));
-    r[2] = as_u32(as_h2((q8 & 0x000f000fu) | 0x64006400u) - as_h2(z1024));
-    r[3] = as_u32(as_h2((q8 & 0x00f000f0u) | 0x64006400u) * sixteenth - as_h2(z64));
-    return r;
-}
-
-// fp16, biased: two bitwise ops per pair, no arithmetic.  Pairs 0 and 2 come
-// out as 1024 + u, pairs 1 and 3 as 1024 + 16u (both exact in fp16).  The
-// caller stages the activations of pairs 1 and 3 pre-multiplied by 1/16 and
-// removes 1024 * sum(a) + z * sum(a * w) per row and K range in fp32, where w
-// is 1 for pairs 0, 2 and 16 for pairs 1, 3.
-__device__ __forceinline__ u32x4 dq_f16_biased(uint32_t q) {
-    const uint32_t q8 = q >> 8;
-    u32x4 r;
-    r[0] = (q & 0x000f000fu) | 0x64006400u;
-    r[1] = (q & 0x00f000f0u) | 0x64006400u;
-    r[2] = (q8 & 0x000f000fu) | 0x64006400u;
-    r[3] = (q8 & 0x00f000f0u) | 0x64006400u;
-    return r;
-}
-
 // fp16 with the group scale folded in (one rounding, like the reference's
 // q*scale -> fp16 B fragment, w4a16_marlin.cu:103-113).  s_lo scales pairs 0,1
 // and s_hi pairs 2,3 (the two 16-K halves of the tile for the MARLIN layout).
