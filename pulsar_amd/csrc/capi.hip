@@ -114,6 +114,19 @@ int decode_splits_override() {
     return (v == 2 || v == 4 || v == 8) ? v : 0;
 }
 
+// Windowed decode plans (one unit per workgroup, the activations staged in K
+// windows by copy waves) where the activation slice does not fit in LDS: by
+// default only in place of the counter path (slices the exchange tree cannot
+// take); PW4_DECODE_WIN=1 takes them wherever they apply, =0 never (A/B
+// sweeps and tests only).
+enum { kWinNever = 0, kWinAlways = 1, kWinForCounter = 2 };
+int decode_win_mode() {
+    const char* e = plan_env("PW4_DECODE_WIN");
+    if (e && e[0] == '0') return kWinNever;
+    if (e && e[0] == '1') return kWinAlways;
+    return kWinForCounter;
+}
+
 // Plan of the 256-wide prefill kernel: tile rows (256 or 128) and K slices,
 // from a cost model in microseconds fitted to a sweep of every (rows, slices)
 // pair over the Llama-3-8B and -70B layer shapes at M = 72..4096 on one MI355X
@@ -268,9 +281,48 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         // 8.7 against 9.2); qkv at M = 24-32 (1.5 slices per CU at 32) stays at
         // 16, and so do slices small enough for two workgroups per CU (down at
         // M = 5: 11.1 us at 16 against 14.3).
+        // Windowed plan instead of K slices: one slice, units of the narrowest
+        // width that gives every workgroup one unit on at least half the CUs
+        // (so the activations are read once per workgroup), the largest K
+        // window whose two buffers fit in LDS with a power-of-two number of
+        // steps per K wave and at least two windows.  Every workgroup reads
+        // the whole M x K activations from L2, against 1/slices of them with
+        // K slices: measured on MI355X (kernel only, us, windowed / sliced),
+        // Llama-3-8B down M = 6-16 12.6-17.2 / 10.0-13.0, M = 24-32 22.4-26.0
+        // / 21.3-23.2, 70B qkv and o M = 9-16 13.3-18.6 / 12.1-16.0, all with
+        // the exchange tree; 70B down M = 32 68.7 / 148.8, where the slices
+        // exceed the tree's eight and take the counter path.
+        const int win_mode = decode_win_mode();
+        int64_t kwin = 0;
+        int win_nb = 16;
+        bool win_red_single = false;
+        if (!forced && s > 1 && layout == LAYOUT_MARLIN && dc.ngrp <= 2 && M <= 32 && K == kext && K % 128 == 0 &&
+            decode_splits_override() == 0 && win_mode != kWinNever) {
+            const int nb_forced = decode_nb_override();
+            for (int w : {16, 32, 64}) {
+                if (ncols % w != 0 || (nb_forced && w != nb_forced)) continue;
+                const int64_t ncg_w = ncols / w;
+                if (ncg_w > cus || 2 * ncg_w <= cus) continue;
+                const int64_t wstep = 128 * (8 / (w / 16));  // K of one step of every K wave
+                for (bool rs1 : {false, true}) {
+                    for (int64_t jw = 64; jw >= 1 && kwin == 0; jw /= 2) {
+                        const int64_t kw = jw * wstep;
+                        if (kw >= kext || kext % kw != 0) continue;
+                        if (decode_lds_bytes((int)M, (int)kw, dc.ngrp, zp_any, bf, rs1, true) > kDecodeLdsLimit) continue;
+                        kwin = kw;
+                        win_red_single = rs1;
+                    }
+                    if (kwin) break;
+                }
+                if (kwin) {
+                    win_nb = w;
+                    break;
+                }
+            }
+        }
         bool tree = false;
         int tree_nb = 16;
-        if (!forced && dc.ngrp <= 2) {  // no exchange-tree variants for groups narrower than 64
+        if (!forced && !(kwin > 0 && win_mode == kWinAlways) && dc.ngrp <= 2) {  // no tree for groups under 64
             int64_t s2 = std::max<int64_t>(s, decode_splits_override());
             if (s2 > 1) {
                 int64_t p2 = 2;
@@ -296,12 +348,17 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
                 }
             }
         }
+        const bool win = kwin > 0 && !tree;
+        if (win) {
+            s = 1;
+            red_single = win_red_single;
+        }
         const int64_t kps = kps_for(s);
         if (!forced && !tree) s = std::max<int64_t>(ceil_div(ktiles * 32, kps), 1);
-        const size_t lds = lds_for(s);
+        const size_t lds = win ? decode_lds_bytes((int)M, (int)kwin, dc.ngrp, zp_any, bf, red_single, true) : lds_for(s);
         // Units: 16 columns (eight K waves per strip, the finest balance), or
         // 64 when K is sliced, to keep the per-unit partial round trips few.
-        int nb = tree ? tree_nb : decode_nb_override();
+        int nb = win ? win_nb : tree ? tree_nb : decode_nb_override();
         if (nb == 0) nb = s > 1 ? 64 : 16;
         while (nb > 16 && ncols % nb != 0) nb /= 2;
         const int64_t ncg = ceil_div(ncols, nb);
@@ -321,7 +378,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         // least per-CU load.
         int64_t per_cu_max =
             lds <= kDecodeLdsLimit
-                ? decode_blocks_per_cu(layout, bf ? X_BF16 : X_F16, stype, zp, dc.mt, dc.ngrp, dc.ring, tree, lds)
+                ? decode_blocks_per_cu(layout, bf ? X_BF16 : X_F16, stype, zp, dc.mt, dc.ngrp, dc.ring, tree, lds, win)
                 : 0;
         if (per_cu_max <= 0) per_cu_max = std::max<int64_t>(std::min<int64_t>(2, (int64_t)(kLdsPerCu / std::max<size_t>(lds, 1))), 1);
         per_cu_max = std::min<int64_t>(per_cu_max, 2);
@@ -340,6 +397,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
             const int64_t v = std::atoll(e);
             if (v >= 1 && v <= 4 * (int64_t)cus) best_wps = std::min<int64_t>(v, ncg);
         }
+        if (win) best_wps = ncg;  // one unit per workgroup
         dc.nb = nb;
         dc.wps = (int)best_wps;
         dc.k_per_split = (int)kps;
@@ -347,6 +405,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         dc.lds_bytes = lds;
         dc.red_single = red_single;
         dc.tree = tree;
+        dc.kwin = win ? (int)kwin : 0;
         const bool partial = !tree && (forced || s > 1);
         if (lds <= kDecodeLdsLimit && !(partial && ncg > kMaxCounterCols) && best_wps * s <= INT32_MAX &&
             s <= 65535) {
@@ -507,13 +566,14 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.ktiles = (int)(kext / 32);
         a.nchunks = (int)(round_up(K, kMarlinBK) / kMarlinBK);
         a.k_per_split = p.dc.k_per_split;
-        a.rowstride = p.dc.k_per_split + 8;
+        a.kwin = p.dc.kwin > 0 ? p.dc.kwin : p.dc.k_per_split;
+        a.rowstride = a.kwin + 8;
+        a.jw_log2 = p.dc.kwin > 0 ? __builtin_ctz((unsigned)(p.dc.kwin / 128 / (8 / (p.dc.nb / 16)))) : 0;
         a.splits = p.dc.splits;
         const int64_t ncols = layout == LAYOUT_MARLIN ? round_up(N, kMarlinBN) : round_up(N, 16);
         a.ncg = (int)ceil_div(ncols, p.dc.nb);
         a.ups = (int)ceil_div(a.ncg, p.dc.wps);
-        a.spr_recip = (uint32_t)(((uint64_t{1} << 32) + (uint64_t)(p.dc.k_per_split / 8 + 1) - 1) /
-                                 (uint64_t)(p.dc.k_per_split / 8 + 1));
+        a.spr_recip = (uint32_t)(((uint64_t{1} << 32) + (uint64_t)(a.kwin / 8 + 1) - 1) / (uint64_t)(a.kwin / 8 + 1));
         e = launch_decode(layout, xt, stype, qzeros != nullptr, p.dc, a, stream, ev);
         if (e != hipSuccess) return hip_fail(e);
     } else {

@@ -57,6 +57,8 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kRing = 8;
+// copy waves of a windowed plan (after the eight compute waves)
+constexpr int kCopyWaves = 4;
 
 // (a & mask) | b for a splice constant b with no bits under the mask.  The
 // masks come from the kernel arguments (see NibbleMasks) and b from a VGPR,
@@ -184,8 +186,8 @@ __host__ __device__ inline size_t red_floats(int mt) { return (size_t)2 * kWaves
 // compiler from moving LDS accesses across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <bool BF16, int LAYOUT, typename ST, int MT, int NGRP, bool ZP, int U, bool TREE>
-__global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
+template <bool BF16, int LAYOUT, typename ST, int MT, int NGRP, bool ZP, int U, bool TREE, bool WIN>
+__global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void decode_kernel(const DecodeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     __shared__ int s_last;
     constexpr int MP = MT * 16;
@@ -225,28 +227,65 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     const int spu = max((nsteps + kwn - 1) >> kwn_log2, 1);
     const int spu_pad = (spu + U - 1) / U * U;  // positions per unit, a whole number of ring blocks
 
-    float* RED = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + x_slots(M, a.k_per_split) * 16);
+    // the staged x: one buffer of the slice, or (WIN) two buffers of a K window
+    const int nslots = (int)x_slots(M, a.kwin);
+    float* RED = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + (size_t)nslots * 16 * (WIN ? 2 : 1));
     const ST* scales = reinterpret_cast<const ST*>(a.scales);
 
     // ---- the activation slice into LDS --------------------------------------
-    // 16-byte slots, row-major over [M][kps/8 + 1] in natural K order (the
+    // 16-byte slots, row-major over [M][kwin/8 + 1] in natural K order (the
     // last slot of a row is padding); each wave instruction fills 64
     // consecutive slots (one global_load_lds_dwordx4) from per-lane global
     // addresses.  Lanes whose slot is past K, past the slice or in the pad are
     // masked off: the copy never writes those slots, and the ones a step
     // reads are zeroed below.
-    const int spr = a.k_per_split / 8 + 1;
-    const int nslots = (int)x_slots(M, a.k_per_split);
+    const int spr = a.kwin / 8 + 1;
     const int kvalid = max(min(klen, K - kb), 0);  // halves of real activations in the slice
-    {
-        const uint32_t smem_base = (uint32_t)(uintptr_t)smem;
-        for (int b = wave; b * 64 < nslots; b += kWaves) {
+    const uint32_t smem_base = (uint32_t)(uintptr_t)smem;
+    // window w of the slice (K kb + w * kwin ..) into buffer w & 1, wave
+    // instructions b0, b0 + bstep, ...; kv: halves of the window to copy
+    auto copy_window = [&](int w, int b0, int bstep, int kv) {
+        const uint32_t base = smem_base + (uint32_t)((w & 1) * nslots * 16);
+        const int64_t k0 = (int64_t)kb + (int64_t)w * a.kwin;
+        for (int b = b0; b * 64 < nslots; b += bstep) {
             const int f = b * 64 + lane;
             const int row = (int)__umulhi((uint32_t)f, a.spr_recip);  // f / spr (exact; checked at launch)
             const int s8 = f - row * spr;
-            if (row < M && s8 * 8 < kvalid) lds_copy16(a.x + (int64_t)row * K + kb + s8 * 8, smem_base + b * 1024);
+            if (row < M && s8 * 8 < kv) lds_copy16(a.x + (int64_t)row * K + k0 + s8 * 8, base + b * 1024);
+        }
+    };
+    if constexpr (WIN) {
+        // Windowed plans (one slice of whole windows, one unit per workgroup,
+        // checked at launch): the eight compute waves copy window 0, and the
+        // kCopyWaves copy waves copy window w + 1 into the other buffer while
+        // they compute window w.  The copies count in the copying waves'
+        // vmcnt only, so the compute waves' weight rings never wait for them;
+        // the waves meet at one barrier per window (the compute waves'
+        // barrier before each window's first step), after which the buffer of
+        // window w - 1 is free.  The copy waves then take part in the unit
+        // end's barriers (one, or two with a single reduction buffer), so
+        // every barrier of the workgroup has all its waves.  One copy wave
+        // was measured 2.2x slower than four (down M = 16 37.9 against 17.2
+        // us): a wave's 1 KB copies in flight do not cover the L2 latency
+        // under a full weight stream.
+        if (wave >= kWaves) {
+            const int cwave = wave - kWaves;
+            const int nwin = (nsteps * 128) / a.kwin;
+            if (nwin > 1) copy_window(1, cwave, kCopyWaves, a.kwin);
+            __syncthreads();  // the compute waves' barrier after their window-0 copies
+            for (int w = 1; w < nwin; ++w) {
+                wait_vmcnt<0>();  // window w is in LDS
+                lds_barrier();    // ... and every compute wave is done with window w - 1
+                if (w + 1 < nwin) copy_window(w + 1, cwave, kCopyWaves, a.kwin);
+            }
+            for (int u = 0; u < n_units; ++u) {
+                if (a.red_single) lds_barrier();
+                lds_barrier();
+            }
+            return;
         }
     }
+    copy_window(0, wave, kWaves, WIN ? min(kvalid, a.kwin) : kvalid);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- weight / scale / zero loads of the wave's t-th step ----------------
@@ -317,8 +356,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     } else {
         wait_vmcnt<0>();
     }
-    // zero the slots the steps read past the real activations
-    {
+    // zero the slots the steps read past the real activations (windowed plans
+    // have none: their slice is whole windows of real activations)
+    if constexpr (!WIN) {
         const int zfrom = kvalid / 8, zto = nsteps * 16;
         for (int i = tid; i < M * (zto - zfrom); i += kThreads) {
             const int row = i / (zto - zfrom), s8 = zfrom + (i - row * (zto - zfrom));
@@ -344,7 +384,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     auto compute_step = [&](int u, int j, const Step& in) {
         const int st = kw + j * kwn;
         if (j >= spu || st >= nsteps) return;  // padding, or an uneven K-wave split
-        const int kl = st * 128;
+        int kl = st * 128;
+        if constexpr (WIN) {
+            // step j of each K wave lies in window j / jw; the window's buffer
+            const int win = j >> a.jw_log2;
+            kl = (st - (win << (a.jw_log2 + kwn_log2))) * 128 + (win & 1) * nslots * 8;
+        }
         const int col0 = (wl + u * a.wps) * nb;
         const int ncol_c = min(col0 + cw * 16 + c, N - 1);
         uint32_t zl[NGRP];
@@ -598,6 +643,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     // the loop: a wave cannot retire before its loads return, and a refill
     // branch inside the loop would merge two ring states at its head, which
     // makes the compiler's vmcnt waits wait for half the ring.
+    // WIN: the barrier before each window's first step (see the copy waves)
+    auto win_sync = [&](int j) {
+        if constexpr (WIN) {
+            if (j > 0 && j < spu && (j & ((1 << a.jw_log2) - 1)) == 0) lds_barrier();
+        }
+    };
     const int nblk = spu_pad / U;
     for (int u = 0; u < n_units; ++u) {
         const int refill_blocks = u + 1 < n_units ? nblk : nblk - 1;
@@ -607,6 +658,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
             const int tu = same ? u : u + 1, tj = same ? jb + U : 0;
 #pragma unroll
             for (int i = 0; i < U; ++i) {
+                win_sync(jb + i);
                 compute_step(u, jb + i, ring[i]);
                 load_step(tu, tj + i, ring[i]);
                 // keep the refill right behind its step: without the barrier
@@ -616,7 +668,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
         }
         if (refill_blocks < nblk) {
 #pragma unroll
-            for (int i = 0; i < U; ++i) compute_step(u, (nblk - 1) * U + i, ring[i]);
+            for (int i = 0; i < U; ++i) {
+                win_sync((nblk - 1) * U + i);
+                compute_step(u, (nblk - 1) * U + i, ring[i]);
+            }
         }
         finish_unit(u);
     }
@@ -633,54 +688,66 @@ using DecodeFn = void (*)(const DecodeArgs);
 // M * 16 <= 512): its atomics in the unit loop make the compiler's wait
 // counts for the weight ring more conservative, which the plain variants
 // should not pay for.  Quant groups narrower than 64 K (NGRP 4 and 8) exist
-// for MT 1 and 2, the 4-step ring and no tree only.
-template <bool BF16, int LAYOUT, typename ST, bool ZP, int U, int MT, bool TREE>
+// for MT 1 and 2, the 4-step ring and no tree only.  Windowed variants (WIN)
+// exist for the MARLIN layout, MT 1 and 2 and NGRP 1 and 2, without the tree.
+template <bool BF16, int LAYOUT, typename ST, bool ZP, int U, int MT, bool TREE, bool WIN>
 DecodeFn pick_ngrp(int ngrp) {
     switch (ngrp) {
-        case 1: return decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE>;
-        case 2: return decode_kernel<BF16, LAYOUT, ST, MT, 2, ZP, U, TREE>;
+        case 1: return decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN>;
+        case 2: return decode_kernel<BF16, LAYOUT, ST, MT, 2, ZP, U, TREE, WIN>;
         case 4:
-            if constexpr (!TREE && MT <= 2 && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 4, ZP, U, TREE>;
+            if constexpr (!TREE && !WIN && MT <= 2 && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 4, ZP, U, TREE, WIN>;
             return nullptr;
         case 8:
-            if constexpr (!TREE && MT <= 2 && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 8, ZP, U, TREE>;
+            if constexpr (!TREE && !WIN && MT <= 2 && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 8, ZP, U, TREE, WIN>;
             return nullptr;
         default: return nullptr;
     }
 }
 
 template <bool BF16, int LAYOUT, typename ST, bool ZP, int U>
-DecodeFn pick_mt_u(int mt, int ngrp, bool tree) {
+DecodeFn pick_mt_u(int mt, int ngrp, bool tree, bool win) {
     if (tree) {
-        if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, true>(ngrp);
-        if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, true>(ngrp);
+        if (win) return nullptr;
+        if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, true, false>(ngrp);
+        if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, true, false>(ngrp);
         return nullptr;
     }
-    if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false>(ngrp);
-    if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false>(ngrp);
-    if (mt == 4) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 4, false>(ngrp);
+    if (win) {
+        if constexpr (LAYOUT == LAYOUT_MARLIN) {
+            if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false, true>(ngrp);
+            if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false, true>(ngrp);
+        }
+        return nullptr;
+    }
+    if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false, false>(ngrp);
+    if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false, false>(ngrp);
+    if (mt == 4) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 4, false, false>(ngrp);
     return nullptr;
 }
 
 template <bool BF16, int LAYOUT, typename ST, bool ZP>
-DecodeFn pick_mt(int mt, int ngrp, int ring, bool tree) {
-    return ring == 4 ? pick_mt_u<BF16, LAYOUT, ST, ZP, 4>(mt, ngrp, tree) : pick_mt_u<BF16, LAYOUT, ST, ZP, kRing>(mt, ngrp, tree);
+DecodeFn pick_mt(int mt, int ngrp, int ring, bool tree, bool win) {
+    return ring == 4 ? pick_mt_u<BF16, LAYOUT, ST, ZP, 4>(mt, ngrp, tree, win)
+                     : pick_mt_u<BF16, LAYOUT, ST, ZP, kRing>(mt, ngrp, tree, win);
 }
 
 template <bool BF16>
-DecodeFn pick_layout(int layout, int stype, bool zp, int mt, int ngrp, int ring, bool tree) {
-    if (layout == LAYOUT_CT) return (zp || stype != S_F32) ? nullptr : pick_mt<BF16, LAYOUT_CT, float, false>(mt, ngrp, ring, tree);
-    if (stype == S_F32) {
-        return zp ? pick_mt<BF16, LAYOUT_MARLIN, float, true>(mt, ngrp, ring, tree)
-                  : pick_mt<BF16, LAYOUT_MARLIN, float, false>(mt, ngrp, ring, tree);
+DecodeFn pick_layout(int layout, int stype, bool zp, int mt, int ngrp, int ring, bool tree, bool win) {
+    if (layout == LAYOUT_CT) {
+        return (zp || stype != S_F32) ? nullptr : pick_mt<BF16, LAYOUT_CT, float, false>(mt, ngrp, ring, tree, win);
     }
-    return zp ? pick_mt<BF16, LAYOUT_MARLIN, _Float16, true>(mt, ngrp, ring, tree)
-              : pick_mt<BF16, LAYOUT_MARLIN, _Float16, false>(mt, ngrp, ring, tree);
+    if (stype == S_F32) {
+        return zp ? pick_mt<BF16, LAYOUT_MARLIN, float, true>(mt, ngrp, ring, tree, win)
+                  : pick_mt<BF16, LAYOUT_MARLIN, float, false>(mt, ngrp, ring, tree, win);
+    }
+    return zp ? pick_mt<BF16, LAYOUT_MARLIN, _Float16, true>(mt, ngrp, ring, tree, win)
+              : pick_mt<BF16, LAYOUT_MARLIN, _Float16, false>(mt, ngrp, ring, tree, win);
 }
 
-DecodeFn pick_decode(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree) {
-    return xtype == X_BF16 ? pick_layout<true>(layout, stype, zp, mt, ngrp, ring, tree)
-                           : pick_layout<false>(layout, stype, zp, mt, ngrp, ring, tree);
+DecodeFn pick_decode(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree, bool win) {
+    return xtype == X_BF16 ? pick_layout<true>(layout, stype, zp, mt, ngrp, ring, tree, win)
+                           : pick_layout<false>(layout, stype, zp, mt, ngrp, ring, tree, win);
 }
 
 hipError_t prepare(DecodeFn fn, size_t lds) {
@@ -748,17 +815,17 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
 
 }  // namespace
 
-size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single) {
+size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single, bool windowed) {
     const int mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-    size_t b = x_slots(M, kps) * 16 + red_floats(mt) * 4 / (red_single ? 2 : 1);
+    size_t b = x_slots(M, kps) * 16 * (windowed ? 2 : 1) + red_floats(mt) * 4 / (red_single ? 2 : 1);
     return b;
 }
 
 int decode_threads() { return kThreads; }
 
 int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree,
-                         size_t lds) {
-    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, mt, ngrp, ring, tree);
+                         size_t lds, bool windowed) {
+    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, mt, ngrp, ring, tree, windowed);
     if (fn == nullptr) return 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
@@ -772,7 +839,8 @@ int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int 
     }
     int n = 0;
     if (prepare(fn, lds) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void*)fn, kThreads, lds) != hipSuccess) {
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void*)fn, kThreads + (windowed ? 64 * kCopyWaves : 0), lds) !=
+            hipSuccess) {
         (void)hipGetLastError();  // do not leave the failure for the next launch check to report
         return 0;
     }
@@ -783,15 +851,34 @@ int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int 
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          hipStream_t stream, KernelEvents ev) {
-    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp, cfg.ring, cfg.tree);
+    const bool win = cfg.kwin > 0;
+    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp, cfg.ring, cfg.tree, win);
     if (fn == nullptr) return hipErrorInvalidValue;
     // the kernel maps slots to rows with a multiply-high by spr_recip, exact
     // while slot * spr < 2^32
-    const uint64_t spr = (uint64_t)a.k_per_split / 8 + 1;
-    if (x_slots(a.M, a.k_per_split) * spr >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
+    const uint64_t spr = (uint64_t)a.kwin / 8 + 1;
+    if (a.kwin <= 0 || a.kwin % 128 != 0 || x_slots(a.M, a.kwin) * spr >= (uint64_t{1} << 32)) {
+        return hipErrorInvalidValue;
+    }
+    if (win) {
+        // what the windowed kernel's barrier schedule rests on: one slice of
+        // whole windows of real activations, every K wave the same number of
+        // steps in every window, one unit per workgroup
+        const int kwn = 8 / (a.nb / 16);
+        const int64_t kext = (int64_t)a.ktiles * 32;
+        const int64_t jw = (int64_t)a.kwin / 128 / kwn;
+        if (a.splits != 1 || a.tree_levels != 0 || a.partial != nullptr || a.k_per_split != kext ||
+            kext != a.K || kext % a.kwin != 0 || kext / a.kwin < 2 || jw < 1 || (int64_t{1} << a.jw_log2) != jw ||
+            jw * 128 * kwn != a.kwin || a.ups != 1 || a.wps != a.ncg || a.M > 32) {
+            return hipErrorInvalidValue;
+        }
+    } else if (a.kwin != a.k_per_split) {
+        return hipErrorInvalidValue;
+    }
     hipError_t e = prepare(fn, cfg.lds_bytes);
     if (e != hipSuccess) return e;
-    launch_kernel(fn, dim3(a.wps, a.splits), dim3(kThreads), (uint32_t)cfg.lds_bytes, stream, ev.start, ev.stop, a);
+    launch_kernel(fn, dim3(a.wps, a.splits), dim3(kThreads + (win ? 64 * kCopyWaves : 0)), (uint32_t)cfg.lds_bytes, stream,
+                  ev.start, ev.stop, a);
     return hipGetLastError();
 }
 

@@ -70,7 +70,9 @@ struct DecodeArgs {
     int ktiles;              // 32-wide K tiles present in the weight layout
     int nchunks;             // MARLIN: Kpad / 64
     int k_per_split;         // multiple of 128
-    int rowstride;           // LDS row stride of the staged x, in halves (k_per_split + 8)
+    int rowstride;           // LDS row stride of the staged x, in halves (kwin + 8)
+    int kwin;                // K of the staged x window: k_per_split, or a K window (windowed plans)
+    int jw_log2;             // windowed plans: log2(steps per K wave per window)
     int splits;
     // SiLU-gated output (direct store only): the columns are gate|up
     // interleaved by 8 (fused columns 16j..16j+7 gate, 16j+8..16j+15 up) and
@@ -89,6 +91,11 @@ struct DecodeConfig {
     int ring;    // weight-load ring depth in steps: 4 or 8
     bool red_single;
     bool tree;   // K slices through the exchange tree (splits a power of two, M <= 32)
+    // K window of a windowed plan, 0 for none: one slice, one unit per
+    // workgroup, the activations staged window by window into two LDS buffers
+    // by copy waves beside the eight compute waves (MARLIN layout, M <= 32,
+    // NGRP <= 2)
+    int kwin;
     size_t lds_bytes;
 };
 
@@ -96,12 +103,13 @@ struct DecodeConfig {
 // thread count.
 // red_single: one cross-wave reduction buffer instead of two (one more
 // barrier per unit), for plans whose activation slice leaves no room.
-size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single);
+// windowed: kps is the K window, staged in two buffers.
+size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single, bool windowed = false);
 int decode_threads();
 // Resident decode workgroups per CU for the kernel variant and LDS size
 // (0 when the variant does not exist or the runtime cannot tell).
 int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree,
-                         size_t lds);
+                         size_t lds, bool windowed = false);
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          hipStream_t stream, KernelEvents ev = {});
