@@ -413,20 +413,25 @@ def summarize_traffic(fetch_csv: str, write_csv: str) -> int:
 def summarize_trace(trace_csv: str, steps: int) -> int:
     """Recompute `roofline` from a rocprofv3 --kernel-trace CSV of this bench.
 
-    The roofline leg runs last among the decode launches: per shape, in the sweep
-    order, steps*REPS unarmed calls, then as many armed ones.  So the trace's last
-    16 * 2 * steps * REPS decode_kernel dispatches are that leg; their mean
-    duration per shape, and the algorithmic bytes over the mean of those means,
-    give the figure the bench computes from its own events."""
+    The roofline leg runs last among the fp16-activation decode launches (the
+    bf16 sweep, when it runs, comes after it): per shape, in the sweep order,
+    steps*REPS unarmed calls, then as many armed ones.  So the trace's last
+    16 * 2 * steps * REPS decode_kernel dispatches with fp16 activations (the
+    kernel's first template argument false) are that leg; their mean duration
+    per shape, and the algorithmic bytes over the mean of those means, give the
+    figure the bench computes from its own events."""
     import csv
 
-    rows = [r for r in csv.DictReader(open(trace_csv)) if "decode_kernel" in r["Kernel_Name"]]
+    def fp16_decode(name: str) -> bool:
+        return "decode_kernelILb0E" in name or "decode_kernel<false" in name  # mangled or demangled
+
+    rows = [r for r in csv.DictReader(open(trace_csv)) if fp16_decode(r["Kernel_Name"])]
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     reps = steps * REPS
     shapes = [(m, name, k, n) for m in DECODE_M for name, k, n in LLAMA8B]
     need = len(shapes) * 2 * reps
     if len(rows) < need:
-        print(f"{trace_csv}: {len(rows)} decode dispatches, the roofline leg needs {need}", file=sys.stderr)
+        print(f"{trace_csv}: {len(rows)} fp16 decode dispatches, the roofline leg needs {need}", file=sys.stderr)
         return 1
     leg = rows[-need:]
     per_shape, unarmed_all, armed_all = {}, [], []
@@ -437,7 +442,7 @@ def summarize_trace(trace_csv: str, steps: int) -> int:
         unarmed_all.append(sum(un) / reps)
         armed_all.append(sum(ar) / reps)
     alg = sum(decode_bytes(m, k, n) for m, _, k, n in shapes) / len(shapes)
-    res = {"decode_dispatches_in_trace": len(rows), "roofline_leg_dispatches": need,
+    res = {"fp16_decode_dispatches_in_trace": len(rows), "roofline_leg_dispatches": need,
            "mean_unarmed_us": round(sum(unarmed_all) / len(shapes), 3),
            "mean_armed_us": round(sum(armed_all) / len(shapes), 3),
            "algorithmic_bytes_per_launch": round(alg)}
