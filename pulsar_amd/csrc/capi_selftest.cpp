@@ -326,11 +326,14 @@ int main(int argc, char** argv) {
   Workspace ws;
   bool ok = true;
   // Each case takes a different plan of the library: the decode kernel's
-  // direct store, its K slices summed by the exchange tree, a forced K split
-  // through fp32 partials, a 256-wide prefill tile, the same with a K-slice
-  // combine, and the compressed-tensors kernel with no repack.
+  // direct store, its K slices summed by the exchange tree, its K windows (more
+  // slices than the tree takes: one unit per workgroup, 1024-K windows staged
+  // by copy waves), a forced K split through fp32 partials, a 256-wide prefill
+  // tile, the same with a K-slice combine, and the compressed-tensors kernel
+  // with no repack.
   ok &= marlin_case("marlin decode, direct", Layer(1, 4096, 4096, 128, PW4_DTYPE_F16, 1), 0, ws, st, true);
   ok &= marlin_case("marlin decode, K slices", Layer(8, 1024, 14336, 128, PW4_DTYPE_BF16, 2), 0, ws, st, true);
+  ok &= marlin_case("marlin decode, K windows", Layer(24, 2112, 28672, 128, PW4_DTYPE_F16, 7), 0, ws, st, true);
   ok &= marlin_case("marlin decode, forced split 3", Layer(4, 512, 4096, 128, PW4_DTYPE_F16, 3), 3, ws, st, false);
   ok &= marlin_case("marlin prefill", Layer(300, 1024, 2048, 128, PW4_DTYPE_F16, 4), 0, ws, st, true);
   ok &= marlin_case("marlin prefill, forced split 4", Layer(260, 520, 2048, 64, PW4_DTYPE_BF16, 5), 4, ws, st, false);

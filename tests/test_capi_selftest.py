@@ -45,4 +45,5 @@ def test_selftest_passes_on_gpu():
     assert r.returncode == 0, r.stdout + r.stderr
     assert "all cases passed" in r.stdout
     assert "FAIL" not in r.stdout
-    assert sum(ln.startswith("ok ") for ln in r.stdout.splitlines()) >= 10, r.stdout
+    assert sum(ln.startswith("ok ") for ln in r.stdout.splitlines()) >= 11, r.stdout
+    assert any(ln.startswith("ok ") and "K windows" in ln for ln in r.stdout.splitlines()), r.stdout
