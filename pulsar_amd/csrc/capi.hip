@@ -526,9 +526,7 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         char* rp = ws + kZeroRegion + align_up(p.partial_bytes) + align_up(p.xperm_bytes) + align_up(p.silu_tmp_bytes);
         uint32_t* words = reinterpret_cast<uint32_t*>(rp);
         float* sm = reinterpret_cast<float*>(rp + align_up((size_t)round_up(N, kMarlinBN) * round_up(K, kMarlinBK) / 2));
-        e = launch_repack_ct(w, words, (int)N, (int)K, stream);
-        if (e != hipSuccess) return hip_fail(e);
-        e = launch_scale_transpose(scales, S_F32, sm, (int)N, (int)(K / G), stream);
+        e = launch_repack_ct(w, scales, S_F32, words, sm, (int)N, (int)K, (int)G, stream);
         if (e != hipSuccess) return hip_fail(e);
         layout = LAYOUT_MARLIN;
         w = words;
@@ -704,6 +702,8 @@ int64_t pw4_marlin_words(int64_t N, int64_t K) {
 
 int pw4_repack_w4a16(const int32_t* weight_packed, const void* weight_scale, int scale_dtype, int64_t N, int64_t K,
                      int64_t group_size, int32_t* weight_marlin, float* scale_marlin, pw4_stream_t stream) {
+    // armed timing events: the repack kernel's start and end
+    const KernelEvents ev = take_kernel_events();
     if (N < 0 || K < 0) return PW4_ERR_ARG;
     if (group_size <= 0 || group_size % 16 != 0) return PW4_ERR_SHAPE;
     if (K % 8 != 0 || K % group_size != 0) return PW4_ERR_SHAPE;
@@ -718,10 +718,9 @@ int pw4_repack_w4a16(const int32_t* weight_packed, const void* weight_scale, int
     if (N > 0 && K > 0 && (!weight_packed || !weight_marlin)) return PW4_ERR_ARG;
     if (N > 0 && K > 0 && (!weight_scale || !scale_marlin)) return PW4_ERR_ARG;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    hipError_t e = launch_repack_ct(reinterpret_cast<const uint32_t*>(weight_packed),
-                                    reinterpret_cast<uint32_t*>(weight_marlin), (int)N, (int)K, s);
-    if (e != hipSuccess) return hip_fail(e);
-    e = launch_scale_transpose(weight_scale, st, scale_marlin, (int)N, (int)(K / group_size), s);
+    const hipError_t e = launch_repack_ct(reinterpret_cast<const uint32_t*>(weight_packed), weight_scale, st,
+                                          reinterpret_cast<uint32_t*>(weight_marlin), scale_marlin, (int)N, (int)K,
+                                          (int)group_size, s, ev.start, ev.stop);
     if (e != hipSuccess) return hip_fail(e);
     return PW4_OK;
 }

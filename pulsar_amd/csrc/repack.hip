@@ -45,16 +45,21 @@ __device__ __forceinline__ int64_t marlin_offset(int n, int t, int nchunks) {
 constexpr int kRepackThreads = 256;
 constexpr int kRepackTiles = 16;  // 32-K tiles per workgroup (a multiple of 2: whole MARLIN chunks)
 
-// compressed-tensors [N, K/8] (signed) -> MARLIN.  grid: (Npad/64, Kpad/512 rounded up).
-// Read: item r = (row r / 16, tile r % 16) of the block, 16 lanes per 256-byte run of a
-// row.  Write: item r = (tile r / 64, column r % 64), 64 lanes per 1 KB run.  LDS rows are
-// padded by 16 bytes so the column-wise reads of the write phase spread over the banks.
-// VEC: rows are 16-byte aligned (K % 32 == 0, aligned base), so a whole tile of a row
-// is one 16-byte load; otherwise every tile is read word by word.
-template <bool VEC>
+// compressed-tensors [N, K/8] (signed) -> MARLIN, and the scales [N, K/G] ->
+// scale_marlin [K/G, N] fp32 (w4a16_marlin.cu:177-185) in the same launch.
+// grid: (Npad/64, Kpad/512 rounded up).
+// Words.  Read: item r = (row r / 16, tile r % 16) of the block, 16 lanes per 256-byte
+// run of a row.  Write: item r = (tile r / 64, column r % 64), 64 lanes per 1 KB run.
+// LDS rows are padded by 16 bytes so the column-wise reads of the write phase spread
+// over the banks.  VEC: rows are 16-byte aligned (K % 32 == 0, aligned base), so a
+// whole tile of a row is one 16-byte load; otherwise every tile is read word by word.
+// Scales.  A workgroup writes the groups whose first K lies in its 512-K range, for
+// its 64 columns: 64 consecutive columns per write (one group per workgroup at G = 128).
+template <bool VEC, typename T>
 __global__ __launch_bounds__(kRepackThreads) void repack_ct_kernel(const uint32_t* __restrict__ packed,
-                                                                   uint32_t* __restrict__ wm, int N, int K,
-                                                                   int nchunks) {
+                                                                   uint32_t* __restrict__ wm,
+                                                                   const T* __restrict__ ws, float* __restrict__ sm,
+                                                                   int N, int K, int G, int nchunks) {
     constexpr int kRow = kRepackTiles + 1;  // u32x4 per LDS row
     __shared__ u32x4 tiles[64 * kRow];
     const int n0 = blockIdx.x * 64, t0 = blockIdx.y * kRepackTiles;
@@ -86,6 +91,13 @@ __global__ __launch_bounds__(kRepackThreads) void repack_ct_kernel(const uint32_
         const int tt = r / 64, col = r % 64;
         const int t = t0 + tt;
         if (t < ktiles) *reinterpret_cast<u32x4*>(wm + marlin_offset(n0 + col, t, nchunks)) = tiles[col * kRow + tt];
+    }
+    const int Kg = K / G;
+    const int k_lo = t0 * 32, k_hi = k_lo + kRepackTiles * 32;
+    const int g_lo = (k_lo + G - 1) / G, g_hi = min((k_hi + G - 1) / G, Kg);
+    for (int i = threadIdx.x; i < (g_hi - g_lo) * 64; i += kRepackThreads) {
+        const int g = g_lo + (i >> 6), n = n0 + (i & 63);
+        if (n < N) sm[(int64_t)g * N + n] = load_scale(ws + (int64_t)n * Kg + g);
     }
 }
 
@@ -131,24 +143,6 @@ __global__ __launch_bounds__(kRepackThreads) void repack_gptq_kernel(const uint3
     }
 }
 
-// scale_marlin[g, n] = (float) weight_scale[n, g]   (w4a16_marlin.cu:177-185)
-template <typename T>
-__global__ __launch_bounds__(256) void scale_transpose_kernel(const T* __restrict__ ws, float* __restrict__ sm, int N,
-                                                              int Kg) {
-    __shared__ float tile[32][33];
-    const int g0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
-    for (int r = ty; r < 32; r += 8) {
-        const int n = n0 + r, g = g0 + tx;
-        tile[r][tx] = (n < N && g < Kg) ? load_scale(ws + (int64_t)n * Kg + g) : 0.f;
-    }
-    __syncthreads();
-    for (int r = ty; r < 32; r += 8) {
-        const int g = g0 + r, n = n0 + tx;
-        if (g < Kg && n < N) sm[(int64_t)g * N + n] = tile[tx][r];
-    }
-}
-
 // perm = stable argsort(g_idx) for an act-order checkpoint: one workgroup per
 // group collects, in ascending k, the rows that belong to it.  status bit 0:
 // some group does not hold exactly G rows; bit 1: a group id out of range.
@@ -184,17 +178,30 @@ __global__ __launch_bounds__(256) void gidx_perm_kernel(const int32_t* __restric
 
 }  // namespace
 
-hipError_t launch_repack_ct(const uint32_t* packed, uint32_t* wm, int N, int K, hipStream_t stream) {
+template <typename T>
+void launch_repack_ct_typed(const uint32_t* packed, const T* ws, uint32_t* wm, float* sm, int N, int K, int G,
+                            hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     const int npad = (int)round_up(N, kMarlinBN), kpad = (int)round_up(K, kMarlinBK);
-    if (npad == 0 || kpad == 0) return hipSuccess;
-    // the 16-byte row reads need 16-byte aligned rows: K % 32 == 0 and an aligned base
     const dim3 grid(npad / 64, (unsigned)ceil_div(kpad / 32, kRepackTiles));
+    // the 16-byte row reads need 16-byte aligned rows: K % 32 == 0 and an aligned base
     if ((K % 32) != 0 || (reinterpret_cast<uintptr_t>(packed) & 15) != 0) {
-        hipLaunchKernelGGL(repack_ct_kernel<false>, grid, dim3(kRepackThreads), 0, stream, packed, wm, N, K,
-                           kpad / kMarlinBK);
+        launch_kernel(repack_ct_kernel<false, T>, grid, dim3(kRepackThreads), 0, stream, start, stop, packed, wm, ws,
+                      sm, N, K, G, kpad / kMarlinBK);
     } else {
-        hipLaunchKernelGGL(repack_ct_kernel<true>, grid, dim3(kRepackThreads), 0, stream, packed, wm, N, K,
-                           kpad / kMarlinBK);
+        launch_kernel(repack_ct_kernel<true, T>, grid, dim3(kRepackThreads), 0, stream, start, stop, packed, wm, ws,
+                      sm, N, K, G, kpad / kMarlinBK);
+    }
+}
+
+hipError_t launch_repack_ct(const uint32_t* packed, const void* ws, int stype_in, uint32_t* wm, float* sm, int N,
+                            int K, int G, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+    if (N == 0 || K == 0) return hipSuccess;
+    if (G <= 0 || K % G != 0) return hipErrorInvalidValue;
+    switch (stype_in) {
+        case 0: launch_repack_ct_typed(packed, reinterpret_cast<const float*>(ws), wm, sm, N, K, G, stream, start, stop); break;
+        case 1: launch_repack_ct_typed(packed, reinterpret_cast<const _Float16*>(ws), wm, sm, N, K, G, stream, start, stop); break;
+        case 2: launch_repack_ct_typed(packed, reinterpret_cast<const __bf16*>(ws), wm, sm, N, K, G, stream, start, stop); break;
+        default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -208,27 +215,6 @@ hipError_t launch_repack_gptq(const uint32_t* qweight, const int32_t* perm, uint
     return hipGetLastError();
 }
 
-hipError_t launch_scale_transpose(const void* ws, int stype_in, float* sm, int N, int Kg, hipStream_t stream) {
-    if (N == 0 || Kg == 0) return hipSuccess;
-    const dim3 grid((unsigned)ceil_div(Kg, 32), (unsigned)ceil_div(N, 32));
-    switch (stype_in) {
-        case 0:
-            hipLaunchKernelGGL(scale_transpose_kernel<float>, grid, dim3(256), 0, stream,
-                               reinterpret_cast<const float*>(ws), sm, N, Kg);
-            break;
-        case 1:
-            hipLaunchKernelGGL(scale_transpose_kernel<_Float16>, grid, dim3(256), 0, stream,
-                               reinterpret_cast<const _Float16*>(ws), sm, N, Kg);
-            break;
-        case 2:
-            hipLaunchKernelGGL(scale_transpose_kernel<__bf16>, grid, dim3(256), 0, stream,
-                               reinterpret_cast<const __bf16*>(ws), sm, N, Kg);
-            break;
-        default:
-            return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
 
 hipError_t launch_gidx_perm(const int32_t* g_idx, int32_t* perm, int32_t* status, int K, int G, hipStream_t stream) {
     if (K == 0) return hipSuccess;

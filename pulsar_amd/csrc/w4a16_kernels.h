@@ -162,10 +162,14 @@ hipError_t launch_prefill256(int xtype, int stype, bool zp, const PrefillArgs& a
 hipError_t launch_gather_x(const uint16_t* x, const int32_t* perm, uint16_t* out, int M, int K, hipStream_t stream);
 
 // Repack kernels.
-hipError_t launch_repack_ct(const uint32_t* packed, uint32_t* wm, int N, int K, hipStream_t stream);
+// Compressed-tensors words [N, K/8] -> MARLIN words, and scales [N, K/G]
+// (stype_in 0 fp32, 1 fp16, 2 bf16) -> fp32 [K/G, N], in one launch.
+// `start` / `stop`: events the launch hands to hipExtLaunchKernel (the
+// dispatch's start / end timestamps), or null.
+hipError_t launch_repack_ct(const uint32_t* packed, const void* ws, int stype_in, uint32_t* wm, float* sm, int N,
+                            int K, int G, hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 hipError_t launch_repack_gptq(const uint32_t* qweight, const int32_t* perm, uint32_t* wm, int N, int K,
                               hipStream_t stream);
-hipError_t launch_scale_transpose(const void* ws, int stype_in, float* sm, int N, int Kg, hipStream_t stream);
 hipError_t launch_gidx_perm(const int32_t* g_idx, int32_t* perm, int32_t* status, int K, int G, hipStream_t stream);
 
 }  // namespace pw4
