@@ -464,10 +464,12 @@ def stack_bench(torch, dev, steps: int, warmup: int) -> dict:
     layers = random_layers(STACK_LAYERS, device=dev, seed=0, stats=rep)
     out = {"layers": STACK_LAYERS, "linears_per_layer": len(layers[0]),
            "repack_at_load": {"linears": STACK_LAYERS * len(layers[0]), "ms": round(rep["repack_ms"], 2),
+                              "call_ms": round(rep["repack_call_ms"], 2),
                               "bytes": rep["repack_bytes"],
                               "GB/s": round(rep["repack_bytes"] / (rep["repack_ms"] * 1e-3) / 1e9, 1),
-                              "note": "GPTQ qweight -> MARLIN words, qweight read + words written, per-linear "
-                                      "HIP events"},
+                              "note": "GPTQ qweight -> MARLIN words, qweight read + words written; ms: the "
+                                      "repack kernels' own intervals (pw4_time_next_kernel), call_ms: HIP events "
+                                      "around each W4A16Linear.from_gptq, host time included"},
            "weight_bytes": sum(l.weight_marlin.numel() * 4 + l.scales.numel() * 2 for ly in layers for l in ly),
            "note": "m1/m32: the 7 linears per layer as 7 launches; fused_m1/fused_m32: q|k|v and gate|up "
                    "N-concatenated (4 launches per layer, same weights and outputs); gated_m1/gated_m32: "

@@ -61,18 +61,19 @@ const char* pw4_status_string(int status);
 const char* pw4_last_hip_error(void);
 /* Kernel timing (no counterpart in the reference; a profiling facility).
  * Arms the calling thread for its next GEMM or repack call (pw4_gemm_w4a16,
- * pw4_gemm_w4a16_marlin, pw4_gemm_w4a16_silu_mul or pw4_repack_w4a16): that
- * call takes the two events (hipEvent_t, created with timing enabled on the
- * call's device) before it checks its arguments, so they never outlive it,
- * and launches its kernels through hipExtLaunchKernel with them.  GEMM:
- * `start` takes the start of the first GEMM dispatch, `stop` the end of the
- * last -- the interval a kernel trace reports, without the queue latency in
- * front of the kernel; a repack, gather, split-K combine or SiLU pass of the
- * call is not inside it.  pw4_repack_w4a16: `start` and `stop` take the start
- * and end of its repack kernel (words and scales in one dispatch).  A call
- * that fails or launches nothing leaves the events unset.  Read them with
- * hipEventElapsedTime after the stream syncs.  (NULL, NULL) disarms; exactly
- * one NULL is PW4_ERR_ARG.  Not for use under graph capture. */
+ * pw4_gemm_w4a16_marlin, pw4_gemm_w4a16_silu_mul, pw4_repack_w4a16 or
+ * pw4_repack_gptq): that call takes the two events (hipEvent_t, created with
+ * timing enabled on the call's device) before it checks its arguments, so
+ * they never outlive it, and launches its kernels through hipExtLaunchKernel
+ * with them.  GEMM: `start` takes the start of the first GEMM dispatch,
+ * `stop` the end of the last -- the interval a kernel trace reports, without
+ * the queue latency in front of the kernel; a repack, gather, split-K combine
+ * or SiLU pass of the call is not inside it.  Repack: `start` and `stop` take
+ * the start and end of the repack kernel (pw4_repack_w4a16: words and scales
+ * in one dispatch).  A call that fails or launches nothing leaves the events
+ * unset.  Read them with hipEventElapsedTime after the stream syncs.
+ * (NULL, NULL) disarms; exactly one NULL is PW4_ERR_ARG.  Not for use under
+ * graph capture. */
 int pw4_time_next_kernel(void* start_event, void* stop_event);
 
 /* ABI version of this header: bumped on any incompatible change. */

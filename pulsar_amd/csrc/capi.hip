@@ -840,12 +840,14 @@ int pw4_gidx_to_perm(const int32_t* g_idx, int64_t K, int64_t group_size, int32_
 
 int pw4_repack_gptq(const int32_t* qweight, const int32_t* perm, int64_t N, int64_t K, int32_t* weight_marlin,
                     pw4_stream_t stream) {
+    // armed timing events: the repack kernel's start and end
+    const KernelEvents ev = take_kernel_events();
     if (N < 0 || K < 0 || N > INT32_MAX || K > INT32_MAX) return PW4_ERR_ARG;
     if (K % 8 != 0) return PW4_ERR_SHAPE;
     if (N > 0 && K > 0 && (!qweight || !weight_marlin)) return PW4_ERR_ARG;
     hipError_t e = launch_repack_gptq(reinterpret_cast<const uint32_t*>(qweight), perm,
                                       reinterpret_cast<uint32_t*>(weight_marlin), (int)N, (int)K,
-                                      reinterpret_cast<hipStream_t>(stream));
+                                      reinterpret_cast<hipStream_t>(stream), ev.start, ev.stop);
     if (e != hipSuccess) return hip_fail(e);
     return PW4_OK;
 }

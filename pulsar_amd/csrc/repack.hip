@@ -207,11 +207,11 @@ hipError_t launch_repack_ct(const uint32_t* packed, const void* ws, int stype_in
 }
 
 hipError_t launch_repack_gptq(const uint32_t* qweight, const int32_t* perm, uint32_t* wm, int N, int K,
-                              hipStream_t stream) {
+                              hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     const int npad = (int)round_up(N, kMarlinBN), kpad = (int)round_up(K, kMarlinBK);
     if (npad == 0 || kpad == 0) return hipSuccess;
-    hipLaunchKernelGGL(repack_gptq_kernel, dim3(npad / 64, (unsigned)ceil_div(kpad / 32, kRepackTiles)),
-                       dim3(kRepackThreads), 0, stream, qweight, perm, wm, N, K, kpad / kMarlinBK);
+    launch_kernel(repack_gptq_kernel, dim3(npad / 64, (unsigned)ceil_div(kpad / 32, kRepackTiles)),
+                  dim3(kRepackThreads), 0, stream, start, stop, qweight, perm, wm, N, K, kpad / kMarlinBK);
     return hipGetLastError();
 }
 

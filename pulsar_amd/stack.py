@@ -26,6 +26,7 @@ from __future__ import annotations
 
 import torch
 
+from . import capi
 from .linear import W4A16Linear, W4A16SiluGate
 
 # (name, K, N) of the seven linears of one Llama-3-8B layer (hidden 4096, 8 KV
@@ -50,11 +51,14 @@ def random_layers(num_layers: int, shapes=LLAMA3_8B_LINEARS, group_size: int = 1
                   seed: int = 0, stats: dict | None = None) -> list[list[W4A16Linear]]:
     """Random symmetric int4 GPTQ weights (u ~ U{0..15}, zero 8) and |N(0, 0.02)| + 1e-3 fp16
     scales, generated on the device and repacked to the MARLIN layout, as a checkpoint load
-    would.  With `stats`, the repack time and bytes (qweight read, MARLIN words written) are
-    accumulated into stats["repack_ms"] and stats["repack_bytes"]."""
+    would.  With `stats`, the repack bytes (qweight read, MARLIN words written) and times are
+    accumulated: stats["repack_ms"] the repack kernels' own intervals (the library's timing
+    hook, pw4_time_next_kernel, armed for each repack), stats["repack_call_ms"] HIP events
+    around each from_gptq call, which also hold its host time."""
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
-    events = []
+    lib = capi() if stats is not None else None
+    events, kernel_events = [], []
     nbytes = 0
     layers = []
     for _ in range(num_layers):
@@ -63,14 +67,19 @@ def random_layers(num_layers: int, shapes=LLAMA3_8B_LINEARS, group_size: int = 1
             qweight = torch.randint(-(2 ** 31), 2 ** 31, (k // 8, n), dtype=torch.int32, device=device,
                                     generator=gen)
             scales = (torch.randn(k // group_size, n, device=device, generator=gen) * 0.02).abs_().add_(1e-3).half()
-            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) if stats is not None \
-                else None
-            if ev:
+            if lib is not None:
+                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                kev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                for e in kev:
+                    e.record()  # create the events before handing them over
                 ev[0].record()
+                if lib.pw4_time_next_kernel(kev[0], kev[1]) != 0:
+                    raise RuntimeError("pw4_time_next_kernel failed")
             lin = W4A16Linear.from_gptq(qweight, scales, group_size)
-            if ev:
+            if lib is not None:
                 ev[1].record()
                 events.append(ev)
+                kernel_events.append(kev)
                 nbytes += qweight.numel() * 4 + lin.weight_marlin.numel() * 4
             lin.name = name
             layer.append(lin)
@@ -78,7 +87,8 @@ def random_layers(num_layers: int, shapes=LLAMA3_8B_LINEARS, group_size: int = 1
         layers.append(layer)
     if stats is not None:
         torch.cuda.synchronize()
-        stats["repack_ms"] = stats.get("repack_ms", 0.0) + sum(a.elapsed_time(b) for a, b in events)
+        stats["repack_ms"] = stats.get("repack_ms", 0.0) + sum(a.elapsed_time(b) for a, b in kernel_events)
+        stats["repack_call_ms"] = stats.get("repack_call_ms", 0.0) + sum(a.elapsed_time(b) for a, b in events)
         stats["repack_bytes"] = stats.get("repack_bytes", 0) + nbytes
     return layers
 

@@ -69,3 +69,23 @@ def test_armed_repack_times_its_kernels():
     ops.gemm_w4a16_marlin(x, w1, s1, g)
     torch.cuda.synchronize()
     assert ev[2].elapsed_time(ev[3]) == kernel_ms
+
+
+def test_armed_gptq_repack_times_its_kernel():
+    lib = pulsar_amd.capi()
+    n, k, g = 1024, 4096, 128
+    rng = np.random.default_rng(8)
+    qweight = torch.from_numpy(O.pack_gptq(rng.integers(0, 16, size=(n, k)).astype(np.uint8))).cuda()
+    stream = torch.cuda.current_stream()
+    w0, _ = ops.repack_w4a16_gptq(qweight, None, g)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for e in ev:
+        e.record(stream)  # creates the events
+    ev[0].record(stream)
+    assert lib.pw4_time_next_kernel(ev[2], ev[3]) == 0
+    w1, _ = ops.repack_w4a16_gptq(qweight, None, g)
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    kernel_ms, call_ms = ev[2].elapsed_time(ev[3]), ev[0].elapsed_time(ev[1])
+    assert torch.equal(w0, w1)
+    assert 0.0 < kernel_ms <= call_ms
