@@ -19,10 +19,12 @@ GROUP_SIZES = [64, 128]
 
 
 # K % 32 != 0 (144, 48) takes the repack's word-by-word reads; K = 2112 (66 tiles) ends in a
-# partial 16-tile workgroup; 28672 x 4096 is the gate_up layer
+# partial 16-tile workgroup; 28672 x 4096 is the gate_up layer.  Each workgroup also writes
+# the scales of the groups that start in its 512-K range: G = 384 puts two groups in the
+# first range, and G = 80 (with K % 32 != 0) starts groups at every offset within a range.
 @pytest.mark.parametrize("n,k,g", [(128, 256, 64), (100, 144, 48), (4096, 4096, 128), (6144, 4096, 128),
                                    (72, 48, 16), (1000, 2048, 64), (64, 64, 64), (200, 2112, 64),
-                                   (28672, 4096, 128)])
+                                   (28672, 4096, 128), (130, 1536, 384), (96, 1040, 80)])
 @pytest.mark.parametrize("sdtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_repack_bit_exact(n, k, g, sdtype):
     rng = np.random.default_rng(n + k)
