@@ -40,6 +40,10 @@
 // partial tile and the last to arrive for a unit (arrival counter) sums the
 // partials in slice order -- the fixed-order combine of the reference
 // (w4a16_common.cuh:94-120) without a second launch -- and resets the counter.
+// Windowed plans (WIN instantiations), taken where the slices would exceed
+// the tree's eight: no K slices; each workgroup takes one unit over the whole
+// K, and copy waves beside the eight compute waves stage the activations in K
+// windows through two LDS buffers, one barrier per window.
 //
 // Reference counterpart: w4a16_marlin_kernel / gemm_w4a16_kernel at BM = 16
 // (pulsar-core/src/kernels/w4a16_marlin.cu:197-304, w4a16_gemm.cu:153-264).
