@@ -47,6 +47,7 @@ def _operands(lib, hip, p):
 # (M, N, K, num_splits, act_order), each call smaller than the one before
 CALLS = [
     (300, 1040, 2048, 4, False),   # prefill K slices: partials in the scratch, combine
+    (24, 2112, 28672, 0, False),   # decode, K windows (more slices than the tree takes; no scratch)
     (16, 2048, 14336, 0, False),   # decode, exchange-tree K slices in the zero region
     (8, 1024, 8192, 0, True),      # act-order: x[:, perm] gathered into the scratch
     (4, 512, 4096, 3, False),      # decode, forced K slices: counters + partials
