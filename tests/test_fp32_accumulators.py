@@ -13,7 +13,7 @@ PW4_ZERO_REGION_BYTES zero region, and the last arriving slice (decode) or the c
     prefill [slices][M][N]);
   * the partials summed in float64 are the accumulators over the whole K, held to max-abs
     1e-2 against x @ dequant(W)^T in float64 (exact: the fp16 x and the dequantised weights
-    (u - 8) * s are fp32 values, and so are their products).
+    (u - z) * s are fp32 values, and so are their products).
 Reference counterparts: the split paths behind gemm_w4a16_split / gemm_w4a16_marlin
 (pulsar-core/src/kernels/w4a16_gemm.cu:355-489, w4a16_common.cuh:94-120); the bar is the
 north star's max-abs 1e-2.
@@ -31,14 +31,17 @@ pytestmark = pytest.mark.gpu
 G = 128
 MAX_ABS = 1e-2
 
-# (plan, M, N, K, slices, bf16 x): the decode kernel's counter path and the 256-wide prefill
-# kernel's split (exact scaling with fp16 x), at the long-K layers of Llama-3-8B and -70B
+# (plan, M, N, K, slices, bf16 x, act-order): the decode kernel's counter path and the
+# 256-wide prefill kernel's split (exact scaling with fp16 x), at the long-K layers of
+# Llama-3-8B and -70B; act-order is config 4's asymmetric int4 with a g_idx permutation
 CASES = [
-    ("decode", 16, 4096, 14336, 4, False),
-    ("decode", 1, 2048, 28672, 8, False),
-    ("decode", 8, 1024, 14336, 2, True),
-    ("prefill", 256, 2048, 14336, 4, False),
-    ("prefill", 128, 1024, 28672, 8, False),
+    ("decode", 16, 4096, 14336, 4, False, False),
+    ("decode", 1, 2048, 28672, 8, False, False),
+    ("decode", 8, 1024, 14336, 2, True, False),
+    ("decode", 16, 1024, 28672, 8, False, True),
+    ("prefill", 256, 2048, 14336, 4, False, False),
+    ("prefill", 128, 1024, 28672, 8, False, False),
+    ("prefill", 128, 1024, 28672, 4, False, True),
 ]
 
 
@@ -50,25 +53,35 @@ def env():
     hip.free_all()
 
 
-@pytest.mark.parametrize("plan,m,n,k,slices,bf16", CASES)
-def test_pre_cast_accumulators(env, plan, m, n, k, slices, bf16):
+@pytest.mark.parametrize("plan,m,n,k,slices,bf16,act", CASES)
+def test_pre_cast_accumulators(env, plan, m, n, k, slices, bf16, act):
     lib, hip = env
-    what = f"{plan} M={m} N={n} K={k} slices={slices} {'bf16' if bf16 else 'fp16'}"
+    what = f"{plan} M={m} N={n} K={k} slices={slices} {'bf16' if bf16 else 'fp16'}{' act-order' if act else ''}"
     print(what, flush=True)
-    p = O.make_problem(m, n, k, G, seed=m + n + k, bf16=bf16)
-    packed = hip.upload(p.ct_packed())
-    sc = hip.upload(p.scale_nk.astype(np.float32))
+    p = O.make_problem(m, n, k, G, seed=m + n + k, bf16=bf16, symmetric=not act, act_order=act)
     wm = hip.malloc(lib.pw4_marlin_words(n, k) * 4)
-    sm = hip.malloc(n * (k // G) * 4)
-    assert lib.pw4_repack_w4a16(packed, sc, DTYPE_F32, n, k, G, wm, sm, None) == 0
+    if act:
+        # GPTQ words repacked in the permuted K order, fp16 [K/G, N] scales, int4 zero points
+        gi = hip.upload(p.g_idx.astype(np.int32))
+        perm = hip.malloc(k * 4)
+        status = hip.malloc(4)
+        assert lib.pw4_gidx_to_perm(gi, k, G, perm, status, None) == 0
+        assert hip.download(status, (1,), np.int32)[0] == 0
+        assert lib.pw4_repack_gptq(hip.upload(p.qweight()), perm, n, k, wm, None) == 0
+        sm, sdt, qz = hip.upload(O.f32_to_f16_bits(p.scale_kn)), DTYPE_F16, hip.upload(p.qzeros())
+    else:
+        packed = hip.upload(p.ct_packed())
+        sc = hip.upload(p.scale_nk.astype(np.float32))
+        sm, sdt, qz, perm = hip.malloc(n * (k // G) * 4), DTYPE_F32, None, None
+        assert lib.pw4_repack_w4a16(packed, sc, DTYPE_F32, n, k, G, wm, sm, None) == 0
     x = hip.upload(p.x16)
     y = hip.malloc(m * n * 2)
-    ws_bytes = lib.pw4_gemm_w4a16_marlin_workspace_size(m, n, k, G, 0, slices)
+    ws_bytes = lib.pw4_gemm_w4a16_marlin_workspace_size(m, n, k, G, int(act), slices)
     assert ws_bytes >= PW4_ZERO_REGION_BYTES + slices * m * n * 4
     ws = hip.malloc(ws_bytes)
     hip.memset(ws, 0, ws_bytes)
     dt = DTYPE_BF16 if bf16 else DTYPE_F16
-    rc = lib.pw4_gemm_w4a16_marlin(x, dt, wm, sm, DTYPE_F32, None, None, y, m, n, k, G, slices, ws, ws_bytes, None)
+    rc = lib.pw4_gemm_w4a16_marlin(x, dt, wm, sm, sdt, qz, perm, y, m, n, k, G, slices, ws, ws_bytes, None)
     assert rc == 0, (what, lib.pw4_status_string(rc), lib.pw4_last_hip_error())
     raw = hip.download(ws, (ws_bytes // 4,), np.float32)[PW4_ZERO_REGION_BYTES // 4:]
     if plan == "decode":
