@@ -847,7 +847,7 @@ int pw4_repack_gptq(const int32_t* qweight, const int32_t* perm, int64_t N, int6
     if (N > 0 && K > 0 && (!qweight || !weight_marlin)) return PW4_ERR_ARG;
     hipError_t e = launch_repack_gptq(reinterpret_cast<const uint32_t*>(qweight), perm,
                                       reinterpret_cast<uint32_t*>(weight_marlin), (int)N, (int)K,
-                                      reinterpret_cast<hipStream_t>(stream), ev.start, ev.stop);
+                                      reinterpret_cast<hipStream_t>(stream), ev.start, ev.stop, cu_count());
     if (e != hipSuccess) return hip_fail(e);
     return PW4_OK;
 }

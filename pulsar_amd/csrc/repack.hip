@@ -143,6 +143,65 @@ __global__ __launch_bounds__(kRepackThreads) void repack_gptq_kernel(const uint3
     }
 }
 
+// GPTQ qweight [K/8, N] -> MARLIN through the act-order permutation: a
+// workgroup takes NB columns over the whole K.  It stages the columns' source
+// words (all K/8 rows) and the permutation (clamped to [0, K), 16 bits) in LDS,
+// then assembles the MARLIN words from nibbles gathered in LDS, so each source
+// word is read from HBM once (gathering straight from qweight reads it once per
+// nibble).  A thread takes 4 adjacent columns of one 32-K tile: each 8-entry run
+// of the permutation is one 16-byte LDS read shared by the tile's threads, and
+// each source row one 16-byte read for the 4 columns.  grid: Npad/NB.
+constexpr int kPermThreads = 512;
+template <int NB>
+__global__ __launch_bounds__(kPermThreads) void repack_gptq_perm_kernel(const uint32_t* __restrict__ qweight,
+                                                                        const int32_t* __restrict__ perm,
+                                                                        uint32_t* __restrict__ wm, int N, int K,
+                                                                        int nchunks) {
+    static_assert(NB % 4 == 0, "4 columns per thread");
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds_words[];
+    const int k8 = K >> 3;
+    uint32_t* sq = lds_words;                                      // [K/8][NB]
+    uint16_t* sp = reinterpret_cast<uint16_t*>(lds_words + k8 * NB);  // [Kpad]
+    const int kpad = nchunks * 64;
+    const int n0 = blockIdx.x * NB;
+    for (int i = threadIdx.x; i < k8 * NB; i += kPermThreads) {
+        const int r = i / NB, c = i % NB;
+        sq[i] = n0 + c < N ? qweight[(int64_t)r * N + n0 + c] : 0x88888888u;  // padding columns: nibble 8
+    }
+    // padding rows (k >= K) point at row 0 and are masked below
+    for (int k = threadIdx.x; k < kpad; k += kPermThreads) {
+        sp[k] = k < K ? (uint16_t)min(max(perm[k], 0), K - 1) : (uint16_t)0;  // clamped: a bad perm cannot fault
+    }
+    __syncthreads();
+    constexpr int kQuads = NB / 4;  // threads per tile
+    const int ktiles = nchunks * 2;
+    for (int i = threadIdx.x; i < ktiles * kQuads; i += kPermThreads) {
+        const int t = i / kQuads, c0 = (i % kQuads) * 4;
+        uint32_t src[4][4];  // [column][32-bit run j]
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int kb = t * 32 + j * 8;
+            const u32x4 pk = *reinterpret_cast<const u32x4*>(sp + kb);  // 8 permutation entries
+            uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int sk = (pk[e >> 1] >> (16 * (e & 1))) & 0xffff;
+                const u32x4 row = *reinterpret_cast<const u32x4*>(sq + (sk >> 3) * NB + c0);
+                const int sh = 4 * (sk & 7);
+                const bool pad = kb + e >= K;  // padding rows: nibble 8
+#pragma unroll
+                for (int q = 0; q < 4; ++q) w[q] |= (pad ? 8u : (row[q] >> sh) & 0xfu) << (4 * e);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) src[q][j] = w[q];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            *reinterpret_cast<u32x4*>(wm + marlin_offset(n0 + c0 + q, t, nchunks)) = transpose_tile_bytes(src[q]);
+        }
+    }
+}
+
 // perm = stable argsort(g_idx) for an act-order checkpoint: one workgroup per
 // group collects, in ascending k, the rows that belong to it.  status bit 0:
 // some group does not hold exactly G rows; bit 1: a group id out of range.
@@ -206,10 +265,49 @@ hipError_t launch_repack_ct(const uint32_t* packed, const void* ws, int stype_in
     return hipGetLastError();
 }
 
+namespace {
+template <int NB>
+hipError_t launch_repack_gptq_perm(const uint32_t* qweight, const int32_t* perm, uint32_t* wm, int N, int K,
+                                   int npad, int kpad, size_t lds, hipStream_t stream, hipEvent_t start,
+                                   hipEvent_t stop) {
+    const auto fn = repack_gptq_perm_kernel<NB>;
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    launch_kernel(fn, dim3(npad / NB), dim3(kPermThreads), (uint32_t)lds, stream, start, stop, qweight, perm, wm, N,
+                  K, kpad / kMarlinBK);
+    return hipGetLastError();
+}
+}  // namespace
+
 hipError_t launch_repack_gptq(const uint32_t* qweight, const int32_t* perm, uint32_t* wm, int N, int K,
-                              hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+                              hipStream_t stream, hipEvent_t start, hipEvent_t stop, int cus) {
     const int npad = (int)round_up(N, kMarlinBN), kpad = (int)round_up(K, kMarlinBK);
     if (npad == 0 || kpad == 0) return hipSuccess;
+    if (perm != nullptr && K <= 65535) {
+        // act-order through LDS: the widest column block whose source words and
+        // permutation fit and that still gives every CU a workgroup, else the
+        // narrowest that fits
+        constexpr size_t kLdsCap = 152 * 1024;
+        int nb = 0;
+        for (int w : {64, 32, 16, 8, 4}) {
+            const size_t lds = (size_t)(K / 8) * w * 4 + (size_t)kpad * 2;
+            if (lds > kLdsCap) continue;
+            nb = w;
+            if (npad / w >= cus) break;
+        }
+        if (nb != 0) {
+            const size_t lds = (size_t)(K / 8) * nb * 4 + (size_t)kpad * 2;
+            switch (nb) {
+                case 64: return launch_repack_gptq_perm<64>(qweight, perm, wm, N, K, npad, kpad, lds, stream, start, stop);
+                case 32: return launch_repack_gptq_perm<32>(qweight, perm, wm, N, K, npad, kpad, lds, stream, start, stop);
+                case 16: return launch_repack_gptq_perm<16>(qweight, perm, wm, N, K, npad, kpad, lds, stream, start, stop);
+                case 8: return launch_repack_gptq_perm<8>(qweight, perm, wm, N, K, npad, kpad, lds, stream, start, stop);
+                default: return launch_repack_gptq_perm<4>(qweight, perm, wm, N, K, npad, kpad, lds, stream, start, stop);
+            }
+        }
+    }
     launch_kernel(repack_gptq_kernel, dim3(npad / 64, (unsigned)ceil_div(kpad / 32, kRepackTiles)),
                   dim3(kRepackThreads), 0, stream, start, stop, qweight, perm, wm, N, K, kpad / kMarlinBK);
     return hipGetLastError();
