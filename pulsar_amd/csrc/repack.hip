@@ -205,32 +205,48 @@ __global__ __launch_bounds__(kPermThreads) void repack_gptq_perm_kernel(const ui
 // perm = stable argsort(g_idx) for an act-order checkpoint: one workgroup per
 // group collects, in ascending k, the rows that belong to it.  status bit 0:
 // some group does not hold exactly G rows; bit 1: a group id out of range.
+// The entries are ranked 256 at a time in k order (ballot and popcount within a
+// wave, counts of the earlier waves through LDS); a thread loads its entries of
+// kGidxBatch such steps at once, so a step costs one barrier rather than a
+// memory round trip, and the wave counts are double buffered so that one
+// barrier per step suffices.
+constexpr int kGidxBatch = 16;
 __global__ __launch_bounds__(256) void gidx_perm_kernel(const int32_t* __restrict__ g_idx, int32_t* __restrict__ perm,
                                                         int32_t* __restrict__ status, int K, int G) {
-    __shared__ int wave_cnt[4];
+    __shared__ int wave_cnt[2][4];
     const int g = blockIdx.x;
     const int Kg = K / G;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     int base_count = 0;
-    for (int k0 = 0; k0 < K; k0 += 256) {
-        const int k = k0 + tid;
-        const int gv = k < K ? g_idx[k] : -1;
-        if (g == 0 && k < K && (gv < 0 || gv >= Kg)) atomicOr(status, 2);
-        const bool mine = k < K && gv == g;
-        const uint64_t mask = __ballot(mine);
-        const int before_lane = __popcll(mask & ((1ull << lane) - 1ull));
-        if (lane == 0) wave_cnt[wave] = __popcll(mask);
-        __syncthreads();
-        int before_wave = 0, total = 0;
+    int buf = 0;
+    for (int kb = 0; kb < K; kb += 256 * kGidxBatch) {
+        int gv[kGidxBatch];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            before_wave += w < wave ? wave_cnt[w] : 0;
-            total += wave_cnt[w];
+        for (int b = 0; b < kGidxBatch; ++b) {
+            const int k = kb + b * 256 + tid;
+            gv[b] = k < K ? g_idx[k] : -1;
         }
-        const int pos = base_count + before_wave + before_lane;
-        if (mine && pos < G) perm[(int64_t)g * G + pos] = k;
-        base_count += total;
-        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < kGidxBatch; ++b) {
+            const int k = kb + b * 256 + tid;
+            if (kb + b * 256 >= K) break;  // uniform: every thread leaves at the same step
+            if (g == 0 && k < K && (gv[b] < 0 || gv[b] >= Kg)) atomicOr(status, 2);
+            const bool mine = k < K && gv[b] == g;
+            const uint64_t mask = __ballot(mine);
+            const int before_lane = __popcll(mask & ((1ull << lane) - 1ull));
+            if (lane == 0) wave_cnt[buf][wave] = __popcll(mask);
+            __syncthreads();
+            int before_wave = 0, total = 0;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                before_wave += w < wave ? wave_cnt[buf][w] : 0;
+                total += wave_cnt[buf][w];
+            }
+            const int pos = base_count + before_wave + before_lane;
+            if (mine && pos < G) perm[(int64_t)g * G + pos] = k;
+            base_count += total;
+            buf ^= 1;  // the next step writes the other buffer: no barrier before it
+        }
     }
     if (tid == 0 && base_count != G) atomicOr(status, 1);
 }
