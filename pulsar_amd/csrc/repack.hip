@@ -164,13 +164,36 @@ __global__ __launch_bounds__(kPermThreads) void repack_gptq_perm_kernel(const ui
     uint16_t* sp = reinterpret_cast<uint16_t*>(lds_words + k8 * NB);  // [Kpad]
     const int kpad = nchunks * 64;
     const int n0 = blockIdx.x * NB;
-    for (int i = threadIdx.x; i < k8 * NB; i += kPermThreads) {
-        const int r = i / NB, c = i % NB;
-        sq[i] = n0 + c < N ? qweight[(int64_t)r * N + n0 + c] : 0x88888888u;  // padding columns: nibble 8
+    // staging, kStage loads in flight per thread before their LDS stores (a
+    // store right behind its load would make every step a memory round trip)
+    constexpr int kStage = 8;
+    for (int i0 = threadIdx.x; i0 < k8 * NB; i0 += kPermThreads * kStage) {
+        uint32_t v[kStage];
+#pragma unroll
+        for (int q = 0; q < kStage; ++q) {
+            const int i = i0 + q * kPermThreads;
+            const int r = i / NB, c = i % NB;
+            v[q] = (i < k8 * NB && n0 + c < N) ? qweight[(int64_t)r * N + n0 + c] : 0x88888888u;  // padding: nibble 8
+        }
+#pragma unroll
+        for (int q = 0; q < kStage; ++q) {
+            const int i = i0 + q * kPermThreads;
+            if (i < k8 * NB) sq[i] = v[q];
+        }
     }
     // padding rows (k >= K) point at row 0 and are masked below
-    for (int k = threadIdx.x; k < kpad; k += kPermThreads) {
-        sp[k] = k < K ? (uint16_t)min(max(perm[k], 0), K - 1) : (uint16_t)0;  // clamped: a bad perm cannot fault
+    for (int k0 = threadIdx.x; k0 < kpad; k0 += kPermThreads * kStage) {
+        int v[kStage];
+#pragma unroll
+        for (int q = 0; q < kStage; ++q) {
+            const int k = k0 + q * kPermThreads;
+            v[q] = k < K ? min(max(perm[k], 0), K - 1) : 0;  // clamped: a bad perm cannot fault
+        }
+#pragma unroll
+        for (int q = 0; q < kStage; ++q) {
+            const int k = k0 + q * kPermThreads;
+            if (k < kpad) sp[k] = (uint16_t)v[q];
+        }
     }
     __syncthreads();
     constexpr int kQuads = NB / 4;  // threads per tile
