@@ -1,7 +1,7 @@
 """The kernel timing hook (pw4_time_next_kernel): an armed GEMM call launches the
 decode kernel through hipExtLaunchKernel with the caller's events, which then
-bracket that dispatch alone; an armed repack call brackets its word repack and
-scale transpose.  The output is the same as an unarmed call's, the interval is
+bracket that dispatch alone; an armed repack call brackets its one repack
+dispatch (words and scales together).  The output is the same as an unarmed call's, the interval is
 positive and inside the events recorded around the call, and the arming is used
 up by one call."""
 
