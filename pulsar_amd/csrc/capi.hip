@@ -74,6 +74,13 @@ const char* plan_env(const char* name) {
     return enabled ? std::getenv(name) : nullptr;
 }
 
+// Act-order gather override for tuning sweeps: 1 stages the rows in LDS, 0
+// reads them directly, -1 (unset) = heuristic.
+int gather_staged_override() {
+    const char* e = plan_env("PW4_GATHER_STAGED");
+    return e ? std::atoi(e) : -1;
+}
+
 // Decode column width override (16, 32 or 64) for tuning sweeps; 0 = heuristic.
 int decode_nb_override() {
     const char* e = plan_env("PW4_DECODE_NB");
@@ -229,13 +236,17 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
     const bool forced = num_splits >= 1;
     const bool zp_any = true;  // size the LDS for the asymmetric variant (a few hundred bytes more)
     // The decode kernel takes power-of-two group sizes: 128 K steps hold 128 / G
-    // whole groups (G = 16..64, one masked MFMA per group; G of 16 and 32 up to
-    // M = 32) or lie inside one (G >= 128).
+    // whole groups (G = 16..64, one masked MFMA per group) or lie inside one
+    // (G >= 128).
     const int64_t ngrp = G >= 128 ? 1 : 128 / std::max<int64_t>(G, 1);
-    const bool decode_ok = M <= 64 && G >= 16 && (G & (G - 1)) == 0 && (ngrp <= 2 || M <= 32);
+    // Up to M = 32: from M = 33 the 128-row prefill tile is faster at every
+    // Llama-3 8B and 70B layer (measured on MI355X, kernel only, us, decode at
+    // M = 33 and 64 / prefill at M = 65: 8B gate_up 58 and 136 / 35, down 36
+    // and 145 / 36, 70B gate_up 218 and 852 / 114, down 210 and 1031 / 74).
+    const bool decode_ok = M <= 32 && G >= 16 && (G & (G - 1)) == 0;
     if (decode_ok) {
         DecodeConfig dc{};
-        dc.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+        dc.mt = M <= 16 ? 1 : 2;
         dc.ngrp = (int)ngrp;
         const bool bf = x_dtype == PW4_DTYPE_BF16;
         // Columns the units cover (MARLIN pads N to 64; CT columns past N are
@@ -536,7 +547,7 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
     const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
     const uint16_t* xin = reinterpret_cast<const uint16_t*>(x);
     if (perm) {
-        e = launch_gather_x(xin, perm, xperm, (int)M, (int)K, stream);
+        e = launch_gather_x(xin, perm, xperm, (int)M, (int)K, stream, gather_staged_override());
         if (e != hipSuccess) return hip_fail(e);
         xin = xperm;
     }

@@ -688,22 +688,23 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
 
 using DecodeFn = void (*)(const DecodeArgs);
 
-// The exchange tree is a separate instantiation (MT 1 and 2 only: it needs
-// M * 16 <= 512): its atomics in the unit loop make the compiler's wait
-// counts for the weight ring more conservative, which the plain variants
-// should not pay for.  Quant groups narrower than 64 K (NGRP 4 and 8) exist
-// for MT 1 and 2, the 4-step ring and no tree only.  Windowed variants (WIN)
-// exist for the MARLIN layout, MT 1 and 2 and NGRP 1 and 2, without the tree.
+// Instantiated for MT 1 and 2 (M <= 32; larger M runs the prefill kernels).
+// The exchange tree is a separate instantiation: its atomics in the unit loop
+// make the compiler's wait counts for the weight ring more conservative, which
+// the plain variants should not pay for.  Quant groups narrower than 64 K
+// (NGRP 4 and 8) exist for the 4-step ring without the tree only.  Windowed
+// variants (WIN) exist for the MARLIN layout and NGRP 1 and 2, without the
+// tree.
 template <bool BF16, int LAYOUT, typename ST, bool ZP, int U, int MT, bool TREE, bool WIN>
 DecodeFn pick_ngrp(int ngrp) {
     switch (ngrp) {
         case 1: return decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN>;
         case 2: return decode_kernel<BF16, LAYOUT, ST, MT, 2, ZP, U, TREE, WIN>;
         case 4:
-            if constexpr (!TREE && !WIN && MT <= 2 && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 4, ZP, U, TREE, WIN>;
+            if constexpr (!TREE && !WIN && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 4, ZP, U, TREE, WIN>;
             return nullptr;
         case 8:
-            if constexpr (!TREE && !WIN && MT <= 2 && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 8, ZP, U, TREE, WIN>;
+            if constexpr (!TREE && !WIN && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 8, ZP, U, TREE, WIN>;
             return nullptr;
         default: return nullptr;
     }
@@ -726,7 +727,6 @@ DecodeFn pick_mt_u(int mt, int ngrp, bool tree, bool win) {
     }
     if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false, false>(ngrp);
     if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false, false>(ngrp);
-    if (mt == 4) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 4, false, false>(ngrp);
     return nullptr;
 }
 

@@ -292,6 +292,39 @@ __global__ __launch_bounds__(256) void gather_x_kernel(const uint16_t* __restric
     *reinterpret_cast<uint4*>(out + m * K + j) = make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// The same gather with the source row staged in LDS: workgroup (m, s) copies
+// row m of x into LDS with 16-byte loads, then writes outputs
+// [s * kseg, (s + 1) * kseg) of the row from LDS.  The direct gather above
+// sends every element read to the address path as its own cache line (a
+// random permutation scatters a wave's 64 reads over the whole row); staged,
+// HBM sees the row once and the scattered reads are LDS reads.  Needs a
+// 16-byte aligned x and K * 2 bytes of LDS (checked at launch).
+constexpr int kGatherThreads = 256;
+__global__ __launch_bounds__(kGatherThreads) void gather_x_lds_kernel(const uint16_t* __restrict__ x,
+                                                                      const int32_t* __restrict__ perm,
+                                                                      uint16_t* __restrict__ out, int K, int kseg) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t srow[];
+    const int64_t m = blockIdx.x;
+    const int k8 = K >> 3;
+    const uint4* src = reinterpret_cast<const uint4*>(x + m * K);
+    for (int i = threadIdx.x; i < k8; i += kGatherThreads) reinterpret_cast<uint4*>(srow)[i] = src[i];
+    __syncthreads();
+    const int j_end = min((int)(blockIdx.y + 1) * kseg, K);
+    for (int j = (int)blockIdx.y * kseg + threadIdx.x * 8; j < j_end; j += kGatherThreads * 8) {
+        const int4 p0 = *reinterpret_cast<const int4*>(perm + j);
+        const int4 p1 = *reinterpret_cast<const int4*>(perm + j + 4);
+        const int idx[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        uint32_t v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t lo = srow[min(max(idx[2 * e], 0), K - 1)];  // clamped: a bad perm cannot fault
+            const uint32_t hi = srow[min(max(idx[2 * e + 1], 0), K - 1)];
+            v[e] = lo | (hi << 16);
+        }
+        *reinterpret_cast<uint4*>(out + m * K + j) = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+}
+
 template <bool BF16, int LAYOUT, typename ST, bool ZP>
 hipError_t launch_one(const PrefillArgs& a, hipStream_t stream, KernelEvents ev) {
     const int nwg = (int)(ceil_div(a.M, BM) * ceil_div(a.N, BN));
@@ -325,11 +358,24 @@ hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const Prefi
               : launch_one<false, LAYOUT_MARLIN, _Float16, false>(a, stream, ev);
 }
 
-hipError_t launch_gather_x(const uint16_t* x, const int32_t* perm, uint16_t* out, int M, int K, hipStream_t stream) {
+hipError_t launch_gather_x(const uint16_t* x, const int32_t* perm, uint16_t* out, int M, int K, hipStream_t stream,
+                           int staged) {
     if (K % 8 != 0) return hipErrorInvalidValue;
     const int64_t n = (int64_t)M * (K / 8);
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(gather_x_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, x, perm, out, M, K);
+    const bool fits = K * 2 <= 65536 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)perm & 15) == 0 &&
+                      ((uintptr_t)out & 15) == 0 && M <= 65535;
+    if (staged < 0) staged = M > kGatherStagedMinM;
+    if (staged && fits) {
+        // about 512 workgroups, each segment at least one pass of the block
+        const int ksplit = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(512, M), K / (kGatherThreads * 8)));
+        const int kseg = (int)ceil_div(ceil_div(K, ksplit), 8) * 8;
+        hipLaunchKernelGGL(gather_x_lds_kernel, dim3((unsigned)M, (unsigned)ceil_div(K, kseg)), dim3(kGatherThreads),
+                           (size_t)K * 2, stream, x, perm, out, K, kseg);
+    } else {
+        hipLaunchKernelGGL(gather_x_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, x, perm, out, M,
+                           K);
+    }
     return hipGetLastError();
 }
 

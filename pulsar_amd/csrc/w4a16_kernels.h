@@ -34,7 +34,7 @@ void launch_kernel(F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t st
 enum XType : int { X_F16 = 0, X_BF16 = 1 };
 enum SType : int { S_F32 = 0, S_F16 = 1 };
 
-// Decode GEMM (M <= 64).  The columns are cut into units of nb (16, 32 or
+// Decode GEMM (M <= 32).  The columns are cut into units of nb (16, 32 or
 // 64) and K into `splits` slices; a grid of wps x splits persistent
 // workgroups of 8 waves, workgroup (w, s) taking slice s and the units
 // w, w + wps, w + 2 wps, ...  With more than one slice, each workgroup writes
@@ -84,7 +84,7 @@ struct DecodeArgs {
 struct DecodeConfig {
     int nb;      // columns per unit
     int wps;     // workgroups per K slice
-    int mt;      // 16-row M tiles per wave (1, 2, 4)
+    int mt;      // 16-row M tiles per wave (1 or 2)
     int ngrp;    // quant groups per 128-K step (1 when G % 128 == 0, 2 when G == 64)
     int splits;  // K slices
     int k_per_split;
@@ -158,8 +158,12 @@ int64_t prefill256_tail_cols(int64_t M, int64_t N, int cus, double* waves);
 hipError_t launch_prefill256(int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream,
                              KernelEvents ev = {});
 
-// x_out[m, j] = x[m, perm[j]]
-hipError_t launch_gather_x(const uint16_t* x, const int32_t* perm, uint16_t* out, int M, int K, hipStream_t stream);
+// x_out[m, j] = x[m, perm[j]].  staged: 1 stages each source row in LDS (when
+// K * 2 <= 64 KB and the pointers are 16-byte aligned), 0 reads it directly,
+// -1 picks staged for M > kGatherStagedMinM.
+constexpr int kGatherStagedMinM = 16;
+hipError_t launch_gather_x(const uint16_t* x, const int32_t* perm, uint16_t* out, int M, int K, hipStream_t stream,
+                           int staged = -1);
 
 // Repack kernels.
 // Compressed-tensors words [N, K/8] -> MARLIN words, and scales [N, K/G]
