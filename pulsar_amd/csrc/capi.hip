@@ -143,7 +143,10 @@ int decode_win_mode() {
 //     1.6 us; such tiles run in waves of the CU count, and an unsplit launch
 //     balances its last wave with 128-row tiles;
 //   * 128-row tiles (4 waves) run two workgroups per CU: a chunk takes 1.1 us
-//     on a CU of its own, and a round of two per CU takes 1.6 us;
+//     on a CU of its own, and a round of two per CU takes 1.6 us (a last
+//     round of at most one per CU runs at the solo rate: measured, 70B qkv
+//     8192 x 10240 at M = 2048 343 us on 2 K slices against 372 on the 3
+//     the model picked without it, at M = 4096 579 unsplit against 666 on 2);
 //   * K slices add their fp32 partials' round trip, s * M * N * 8 bytes at
 //     8 TB/s, plus 1 us for the combine launch.
 // fp16 activations with exact scaling use 128-row tiles only: on the same
@@ -184,8 +187,12 @@ Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, b
                 if (s == 1) prefill256_tail_cols(M, N, cus, &waves);
                 us = waves * (double)cps * kChunk256;
             } else {
+                // rounds of two per CU, and a last round of at most one per CU
+                // at the solo rate
                 const int64_t wgs = ceil_div(M, 128) * num_n * s;
-                us = (double)cps * (wgs <= cus ? kChunk128Solo : (double)ceil_div(wgs, 2 * (int64_t)cus) * kChunk128Pair);
+                const int64_t pairs = wgs / (2 * (int64_t)cus), rest = wgs - pairs * 2 * (int64_t)cus;
+                us = (double)cps * ((double)pairs * kChunk128Pair +
+                                    (rest == 0 ? 0.0 : rest <= cus ? kChunk128Solo : kChunk128Pair));
             }
             if (s > 1) us += (double)s * (double)M * (double)N * 8.0 / kPartialBps * 1e6 + kCombineUs;
             if (!have || us < best_us) {
