@@ -6,7 +6,7 @@ M, N, K, the group size, the activation dtype, the weight format and the entry
 point at random (from a fixed seed, so the list is the same on every run), so
 that plan boundaries meet odd shapes: ragged N (not a multiple of 64), K tails
 (not a multiple of 128), M on both sides of the decode/prefill switch and of
-the decode kernel's 16/32/64-row tiles, forced K splits, zero points and
+the decode kernel's 16- and 32-row tiles, forced K splits, zero points and
 act-order.  Entry points, with the reference operator each one replaces:
   * gptq  -- repack_w4a16_gptq + gemm_w4a16_gptq (GPTQ ingestion; no reference
              counterpart, pinned by the oracle's dequantization)

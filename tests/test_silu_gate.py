@@ -103,7 +103,9 @@ CASES = [
     (16, 1024, 1024, torch.float16, {}, True),
     (5, 4160, 256, torch.float16, {}, True),     # N past a 64-column block boundary
     (24, 512, 4096, torch.float16, {}, False),   # decode, exchange-tree K slices
-    (48, 256, 4096, torch.float16, {}, False),   # decode, counter K slices (M > 32)
+    (32, 256, 28672, torch.float16, {"PW4_DECODE_WIN": "0"}, False),  # decode, counter K slices
+    (32, 256, 28672, torch.float16, {}, False),  # decode, K windows where it would take the counter
+    (48, 256, 4096, torch.float16, {}, False),   # 128-row prefill tile, then the SiLU pass (M > 32)
     (300, 1024, 512, torch.float16, {"PW4_PREFILL_SPLITS": "1"}, True),    # 256-wide prefill, unsplit
     (200, 1024, 512, torch.bfloat16, {"PW4_PREFILL_SPLITS": "1"}, False),  # the same, bf16 x
     (129, 512, 2048, torch.float16, {"PW4_PREFILL_SPLITS": "4"}, True),    # 256-wide, K slices -> combine
