@@ -735,26 +735,33 @@ def repack_bench(torch, dev) -> dict:
 
 def dense_yardstick(torch, dev, reps: int) -> dict:
     """What the dense fp16 library GEMM (torch.nn.functional.linear -> hipBLASLt) does at
-    the M = 4096 prefill shapes with the same kind of data (x ~ N(0,1), weights ~ N(0,1)*0.02
-    in fp16): a measured ceiling for the W4A16 prefill next to the nameplate peak."""
+    the prefill shapes (every M of the sweep) with the same kind of data (x ~ N(0,1),
+    weights ~ N(0,1)*0.02 in fp16): a measured ceiling for the W4A16 prefill next to the
+    nameplate peak.  Timed like the W4A16 prefill sweep (events around each call), with the
+    weights rotated over enough copies that each call reads them from HBM, as the W4A16
+    calls do."""
     out = {}
-    m = PREFILL_M[-1]
     for name, k, n in LLAMA8B:
-        x = torch.randn(m, k, device=dev).half()
-        w = (torch.randn(n, k, device=dev) * 0.02).half()
-        for _ in range(2):
-            torch.nn.functional.linear(x, w)
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for a, b in ev:
-            a.record()
-            torch.nn.functional.linear(x, w)
-            b.record()
-        torch.cuda.synchronize()
-        ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
-        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        out[f"{name}_m{m}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
-                               "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3)}
-        del x, w
+        copies = max(1, min(8, -(-(512 << 20) // (n * k * 2))))
+        ws = [(torch.randn(n, k, device=dev) * 0.02).half() for _ in range(copies)]
+        for m in PREFILL_M:
+            x = torch.randn(m, k, device=dev).half()
+            for i in range(2):
+                torch.nn.functional.linear(x, ws[i % copies])
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for i, (a, b) in enumerate(ev):
+                w = ws[i % copies]
+                a.record()
+                torch.nn.functional.linear(x, w)
+                b.record()
+            torch.cuda.synchronize()
+            ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            out[f"{name}_m{m}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+                                   "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3)}
+            del x
+        del ws
+        torch.cuda.empty_cache()
     return out
 
 

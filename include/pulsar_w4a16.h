@@ -76,6 +76,16 @@ const char* pw4_last_hip_error(void);
  * graph capture. */
 int pw4_time_next_kernel(void* start_event, void* stop_event);
 
+/* Diagnostic hook, no counterpart in the reference (it is for parity tests):
+ * arms the calling thread's next GEMM or repack call to also write, into the
+ * device buffer y32 (fp32 [M, N]), the fp32 value each element of y was
+ * rounded from -- the accumulators before the cast to the output dtype -- on
+ * every plan (decode direct store, exchange tree, K-slice counter path,
+ * unsplit prefill kernels, split-K combine) except SiLU-gated calls, which
+ * write no such value.  The call takes the buffer before it checks its
+ * arguments, so it never outlives that call; NULL disarms. */
+int pw4_observe_next_call(float* y32);
+
 /* ABI version of this header: bumped on any incompatible change. */
 int pw4_abi_version(void);
 #define PW4_ABI_VERSION 2
@@ -151,10 +161,16 @@ int pw4_gemm_w4a16_marlin(const void* x, int x_dtype, const int32_t* weight_marl
  * device code (one per device, held until the process exits); a call whose
  * plan needs more returns PW4_ERR_WORKSPACE before launching anything (an
  * automatic prefill plan whose K-slice partials would not fit runs unsplit
- * instead).  The first call on a device clears the array's zero region with a
- * fill kernel on `stream`; every call leaves it zero.  All calls on one device
- * share the array: calls that overlap in time on one device (different
- * streams, or host threads without ordering) race and give wrong results. */
+ * instead).  The array used is the current device's: `stream` must belong to
+ * the current device (PW4_ERR_ARG otherwise).  The first call on a device
+ * clears the array's zero region with a fill kernel on `stream`, and every
+ * call leaves it zero.  When that first call is made under stream capture,
+ * the fill is recorded into the graph once (ahead of the graph's first
+ * no-alloc call, so a replay clears the region before using it) and the next
+ * call outside a capture clears it for good.  All calls on one device share
+ * the array: calls that overlap in time on one device (different streams,
+ * graphs replayed on different streams, or host threads without ordering)
+ * race and give wrong results. */
 #define PW4_NOALLOC_SCRATCH_BYTES (64u << 20)
 int pw4_gemm_w4a16_marlin_noalloc(const void* x, int x_dtype, const int32_t* weight_marlin, const void* scales,
                                   int scale_dtype, const int32_t* qzeros, const int32_t* perm, void* y, int64_t M,

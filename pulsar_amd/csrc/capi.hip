@@ -112,6 +112,14 @@ int prefill_splits_override() {
     return (v >= 1 && v <= 64) ? v : 0;
 }
 
+// Decode kernel override for tuning sweeps: 0 keeps every M off the decode
+// kernel (prefill kernels only), 1 keeps M <= 32 on it; unset = heuristic.
+int decode_mode_override() {
+    const char* e = plan_env("PW4_DECODE");
+    if (!e) return -1;
+    return e[0] == '0' ? 0 : e[0] == '1' ? 1 : -1;
+}
+
 // Decode K-split override for tuning sweeps (2, 4 or 8: exchange-tree
 // slices even where the activations fit in LDS); 0 = heuristic.
 int decode_splits_override() {
@@ -250,7 +258,8 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
     // Llama-3 8B and 70B layer (measured on MI355X, kernel only, us, decode at
     // M = 33 and 64 / prefill at M = 65: 8B gate_up 58 and 136 / 35, down 36
     // and 145 / 36, 70B gate_up 218 and 852 / 114, down 210 and 1031 / 74).
-    const bool decode_ok = M <= 32 && G >= 16 && (G & (G - 1)) == 0;
+    bool decode_ok = M <= 32 && G >= 16 && (G & (G - 1)) == 0;
+    if (decode_mode_override() == 0) decode_ok = false;
     if (decode_ok) {
         DecodeConfig dc{};
         dc.mt = M <= 16 ? 1 : 2;
@@ -568,6 +577,7 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.partial = p.use_partial ? partial : nullptr;
         a.counters = counters;
         a.silu = silu && !silu_tmp ? 1 : 0;
+        a.y32 = silu ? nullptr : ev.y32;
         a.slots = slots;
         a.tree_levels = p.tree ? __builtin_ctz((unsigned)p.dc.splits) : 0;
         a.red_single = p.dc.red_single ? 1 : 0;
@@ -615,13 +625,14 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.cus = cu_count();
         a.tile_rows = p.p_tile_rows;
         a.exact = p.p_exact ? 1 : 0;
+        a.y32 = silu || p.use_partial ? nullptr : ev.y32;
         e = p.p256 ? launch_prefill256(xt, stype, qzeros != nullptr, a, stream, ev)
                    : launch_prefill(layout, xt, stype, qzeros != nullptr, a, stream, ev);
         if (e != hipSuccess) return hip_fail(e);
     }
     if (p.use_partial && !p.decode) {
         e = silu ? launch_combine_silu(partial, reinterpret_cast<uint16_t*>(y), M, N, p.splits, xt, stream)
-                 : launch_combine(partial, reinterpret_cast<uint16_t*>(y), M * N, p.splits, xt, stream);
+                 : launch_combine(partial, reinterpret_cast<uint16_t*>(y), M * N, p.splits, xt, stream, ev.y32);
         if (e != hipSuccess) return hip_fail(e);
     }
     if (silu_tmp) {
@@ -649,21 +660,35 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(u32x4* __restrict__ p, i
 struct DeviceScratch {
     void* ptr = nullptr;    // this device's copy of `scratch`
     bool cleared = false;   // its zero region was cleared by a fill that ran (not one only recorded into a graph)
+    bool fill_captured = false;         // a fill was recorded into the capture `fill_capture_id`
+    unsigned long long fill_capture_id = 0;
 };
 std::mutex g_scratch_mu;
 DeviceScratch g_scratch[kMaxDevices];
 
-// The current device's scratch, set up on the first call on that device: its
-// address, then a fill of the zero region on the caller's stream (a fill
-// kernel, not a memset, so that a capturing caller's graph can hold it).  A
-// fill only recorded into a graph has not run, so the next call from a stream
-// that is not capturing fills again; after that the GEMM kernels keep the
-// region zero.
+// The scratch of the device `stream` runs on, set up on the first call on that
+// device: its address, then a fill of the zero region on the caller's stream
+// (a fill kernel, not a memset, so that a capturing caller's graph can hold
+// it).  The GEMM kernels leave the region zero when they end, so one fill that
+// has run is enough for every later call.  A fill only recorded into a graph
+// has not run: it is recorded once per capture (the graph's first no-alloc
+// call; replays run it ahead of that call's kernels, and the calls after it in
+// the graph find the region as the earlier ones left it), and the next call
+// from a stream that is not capturing fills eagerly.
 int device_scratch(hipStream_t stream, void** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e);
     if (dev < 0 || dev >= kMaxDevices) return PW4_ERR_ARG;
+    // the array is per device: a stream of another device would have its
+    // kernels use memory of the current one (the null stream is the current
+    // device's)
+    if (stream != nullptr) {
+        hipDevice_t sdev = 0;
+        e = hipStreamGetDevice(stream, &sdev);
+        if (e != hipSuccess) return hip_fail(e);
+        if ((int)sdev != dev) return PW4_ERR_ARG;
+    }
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     DeviceScratch& d = g_scratch[dev];
     if (d.ptr == nullptr) {
@@ -674,14 +699,23 @@ int device_scratch(hipStream_t stream, void** out) {
     }
     if (!d.cleared) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        e = hipStreamIsCapturing(stream, &cs);
+        unsigned long long cid = 0;
+        e = hipStreamGetCaptureInfo(stream, &cs, &cid);
         if (e != hipSuccess) return hip_fail(e);
-        const int64_t n16 = (int64_t)(kZeroRegion / 16);
-        hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)ceil_div(n16, 256)), dim3(256), 0, stream,
-                           reinterpret_cast<u32x4*>(d.ptr), n16);
-        e = hipGetLastError();
-        if (e != hipSuccess) return hip_fail(e);
-        d.cleared = cs == hipStreamCaptureStatusNone;
+        const bool capturing = cs == hipStreamCaptureStatusActive;
+        if (!(capturing && d.fill_captured && d.fill_capture_id == cid)) {
+            const int64_t n16 = (int64_t)(kZeroRegion / 16);
+            hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)ceil_div(n16, 256)), dim3(256), 0, stream,
+                               reinterpret_cast<u32x4*>(d.ptr), n16);
+            e = hipGetLastError();
+            if (e != hipSuccess) return hip_fail(e);
+            if (capturing) {
+                d.fill_captured = true;
+                d.fill_capture_id = cid;
+            } else {
+                d.cleared = true;
+            }
+        }
     }
     *out = d.ptr;
     return PW4_OK;
@@ -707,7 +741,13 @@ const char* pw4_last_hip_error(void) { return g_last_hip_error; }
 
 int pw4_time_next_kernel(void* start_event, void* stop_event) {
     if ((start_event == nullptr) != (stop_event == nullptr)) return PW4_ERR_ARG;
-    pw4::g_armed_events = {static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
+    pw4::g_armed_events.start = static_cast<hipEvent_t>(start_event);
+    pw4::g_armed_events.stop = static_cast<hipEvent_t>(stop_event);
+    return PW4_OK;
+}
+
+int pw4_observe_next_call(float* y32) {
+    pw4::g_armed_events.y32 = y32;
     return PW4_OK;
 }
 
@@ -849,9 +889,7 @@ int pw4_gidx_to_perm(const int32_t* g_idx, int64_t K, int64_t group_size, int32_
     if (group_size <= 0 || K % group_size != 0) return PW4_ERR_SHAPE;
     if (!status_dev || (K > 0 && (!g_idx || !perm))) return PW4_ERR_ARG;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    hipError_t e = hipMemsetAsync(status_dev, 0, sizeof(int32_t), s);
-    if (e != hipSuccess) return hip_fail(e);
-    e = launch_gidx_perm(g_idx, perm, status_dev, (int)K, (int)group_size, s);
+    const hipError_t e = launch_gidx_perm(g_idx, perm, status_dev, (int)K, (int)group_size, s);
     if (e != hipSuccess) return hip_fail(e);
     return PW4_OK;
 }

@@ -533,7 +533,10 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
                     if (go) t_old[k + 1][e] = swap_in(k + 1, cg, i, v);
                 } else if (go) {
                     const int row = i >> (4 + cwn_log2), n = cg * nb + (i & (nb - 1));
-                    if (n < N) a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
+                    if (n < N) {
+                        a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
+                        if (a.y32) a.y32[(int64_t)row * N + n] = v;
+                    }
                 }
             }
         }
@@ -601,7 +604,10 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
             for (int i = tid; i < nout; i += kThreads) {
                 const int row = i >> (4 + cwn_log2), n = col0 + (i & (nb - 1));
                 const float v = reduced(i);
-                if (n < N) a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
+                if (n < N) {
+                    a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
+                    if (a.y32) a.y32[(int64_t)row * N + n] = v;
+                }
             }
             return;
         }
@@ -631,7 +637,10 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
                     v += __hip_atomic_load(base + (int64_t)sp * nout + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
                 const int row = i >> (4 + cwn_log2), n = col0 + (i & (nb - 1));
-                if (n < N) a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
+                if (n < N) {
+                    a.y[(int64_t)row * N + n] = f32_to_out<BF16>(v);
+                    if (a.y32) a.y32[(int64_t)row * N + n] = v;
+                }
             }
             if (tid == 0) __hip_atomic_store(a.counters + cg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -763,7 +772,7 @@ hipError_t prepare(DecodeFn fn, size_t lds) {
 // (the prefill path's split-K combine; restates w4a16_common.cuh:97-111).
 template <bool BF16>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ partial, uint16_t* __restrict__ y,
-                                                      int64_t mn, int splits) {
+                                                      int64_t mn, int splits, float* __restrict__ y32) {
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= mn) return;
     if (i + 4 <= mn && (mn & 3) == 0) {
@@ -773,11 +782,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
         o[0] = (uint32_t)f32_to_out<BF16>(s[0]) | ((uint32_t)f32_to_out<BF16>(s[1]) << 16);
         o[1] = (uint32_t)f32_to_out<BF16>(s[2]) | ((uint32_t)f32_to_out<BF16>(s[3]) << 16);
         *reinterpret_cast<u32x2*>(y + i) = o;
+        if (y32) *reinterpret_cast<f32x4*>(y32 + i) = s;
     } else {
         for (int64_t e = i; e < min(i + 4, mn); ++e) {
             float s = 0.f;
             for (int k = 0; k < splits; ++k) s += partial[(int64_t)k * mn + e];
             y[e] = f32_to_out<BF16>(s);
+            if (y32) y32[e] = s;
         }
     }
 }
@@ -914,13 +925,15 @@ hipError_t launch_silu_mul(const uint16_t* h, uint16_t* y, int64_t M, int64_t N,
 }
 
 hipError_t launch_combine(const float* partial, uint16_t* y, int64_t mn, int splits, int xtype,
-                          hipStream_t stream) {
+                          hipStream_t stream, float* y32) {
     const int64_t blocks = ceil_div(ceil_div(mn, 4), 256);
     if (blocks == 0) return hipSuccess;
     if (xtype == X_BF16) {
-        hipLaunchKernelGGL(combine_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, partial, y, mn, splits);
+        hipLaunchKernelGGL(combine_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, partial, y, mn, splits,
+                           y32);
     } else {
-        hipLaunchKernelGGL(combine_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, partial, y, mn, splits);
+        hipLaunchKernelGGL(combine_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, partial, y, mn, splits,
+                           y32);
     }
     return hipGetLastError();
 }

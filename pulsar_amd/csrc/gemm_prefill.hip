@@ -260,6 +260,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) 
                 if (m < M) {
                     if (a.partial == nullptr) {
                         a.y[(int64_t)m * N + n] = f32_to_out<BF16>(acc[mt][nt][e]);
+                        if (a.y32) a.y32[(int64_t)m * N + n] = acc[mt][nt][e];
                     } else {
                         a.partial[((int64_t)split * M + m) * N + n] = acc[mt][nt][e];
                     }

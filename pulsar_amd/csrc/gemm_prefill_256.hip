@@ -415,6 +415,28 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        if (a.y32) {
+            // the accumulators before rounding (pw4_observe_next_call)
+            const __amdgpu_buffer_rsrc_t out32 = __builtin_amdgcn_make_buffer_rsrc(a.y32 + (int64_t)m0 * N, (short)0,
+                                                                                  rows * N * 4, 0x00020000);
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                const int n = ncol0 + (cth * CT + ct) * 32 + c;
+                const uint32_t base = n < N ? (uint32_t)(4 * hb * N + n) * 4u : 0x80000000u;
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int r = rt * 32 + 8 * (e >> 2) + (e & 3);
+                        // copy out first: bit-casting the vector element itself
+                        // reads element 0 (clang)
+                        const float v = acc[rt][ct][e];
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), out32,
+                                                              (int)(base + (uint32_t)(r * N * 4)), 0, 0);
+                    }
+                }
+            }
+        }
     } else {
         const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
             a.partial + ((int64_t)split * M + m0) * N, (short)0, rows * N * 4, 0x00020000);

@@ -193,8 +193,10 @@ at::Tensor W4A16Linear::forward(const at::Tensor& x) const {
     auto x2 = x.reshape({-1, in_}).contiguous();
     at::Tensor y = silu_ ? gemm_w4a16_silu_mul_cuda(x2, weight_marlin_, scales_, qzeros_, perm_, group_size_)
                          : gemm_w4a16_gptq_cuda(x2, weight_marlin_, scales_, qzeros_, perm_, group_size_);
-    // at::linear's bias (qwen2.cpp:78-80): add_ sums the rounded GEMM output and the
-    // bias as stored in fp32 and rounds once to x's dtype
+    // at::linear's bias (qwen2.cpp:78-80).  add_ sums the GEMM output, already
+    // rounded to x's dtype, and the bias in fp32, and rounds the sum again: two
+    // roundings where at::linear rounds x @ W^T + b once (at most one more
+    // rounding of x's dtype per element)
     if (bias_) y.add_(*bias_);
     lead.push_back(out_features());
     return y.view(lead);

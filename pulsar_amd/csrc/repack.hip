@@ -274,6 +274,10 @@ __global__ __launch_bounds__(256) void gidx_perm_kernel(const int32_t* __restric
     if (tid == 0 && base_count != G) atomicOr(status, 1);
 }
 
+__global__ __launch_bounds__(64) void clear_status_kernel(int32_t* __restrict__ status) {
+    if (threadIdx.x == 0) *status = 0;
+}
+
 }  // namespace
 
 template <typename T>
@@ -354,7 +358,11 @@ hipError_t launch_repack_gptq(const uint32_t* qweight, const int32_t* perm, uint
 
 
 hipError_t launch_gidx_perm(const int32_t* g_idx, int32_t* perm, int32_t* status, int K, int G, hipStream_t stream) {
-    if (K == 0) return hipSuccess;
+    // the status word is cleared by a kernel rather than a memset, so that a
+    // caller capturing the stream into a graph records a kernel node
+    hipLaunchKernelGGL(clear_status_kernel, dim3(1), dim3(64), 0, stream, status);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || K == 0) return e;
     hipLaunchKernelGGL(gidx_perm_kernel, dim3(K / G), dim3(256), 0, stream, g_idx, perm, status, K, G);
     return hipGetLastError();
 }

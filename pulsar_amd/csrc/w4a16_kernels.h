@@ -13,10 +13,14 @@ namespace pw4 {
 // last (a split-K combine or SiLU pass after it is not included).  Null: none.
 struct KernelEvents {
     hipEvent_t start = nullptr, stop = nullptr;
+    // pw4_observe_next_call: [M, N] fp32 that receives the accumulators each
+    // y element is rounded from, or null (a diagnostic for the parity tests)
+    float* y32 = nullptr;
 };
 
-// The events armed on the calling thread, which are disarmed: every GEMM entry
-// point takes them first, so they never outlive the call they were armed for.
+// The events (and observation buffer) armed on the calling thread, which are
+// disarmed: every GEMM and repack entry point takes them first, so they never
+// outlive the call they were armed for.
 KernelEvents take_kernel_events();
 
 // hipLaunchKernelGGL, or hipExtLaunchKernelGGL when an event is given (that
@@ -79,6 +83,9 @@ struct DecodeArgs {
     // y is [M, N/2] = silu(gate) * up
     int silu;
     NibbleMasks masks;
+    // [M, N] fp32, or null: the accumulators each stored y element was rounded
+    // from (pw4_observe_next_call; not for SiLU-gated output)
+    float* y32;
 };
 
 struct DecodeConfig {
@@ -113,7 +120,9 @@ int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int 
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          hipStream_t stream, KernelEvents ev = {});
-hipError_t launch_combine(const float* partial, uint16_t* y, int64_t mn, int splits, int xtype, hipStream_t stream);
+// y32: null, or an fp32 copy of each sum before it is rounded into y.
+hipError_t launch_combine(const float* partial, uint16_t* y, int64_t mn, int splits, int xtype, hipStream_t stream,
+                          float* y32 = nullptr);
 // The same fixed-order sum over [splits, M, N] partials of gate|up interleaved
 // columns (N % 16 == 0), writing y [M, N/2] = silu(gate) * up.
 hipError_t launch_combine_silu(const float* partial, uint16_t* y, int64_t M, int64_t N, int splits, int xtype,
@@ -141,6 +150,7 @@ struct PrefillArgs {
     int silu;                // 256-wide kernel, unsplit: y [M, N/2] = silu(gate) * up (see DecodeArgs)
     int exact;               // 256-wide kernel, fp16 x: B = u - z and the scale applied to the fp32
                              // accumulators per group
+    float* y32;              // [M, N] fp32 copy of the unsplit output before rounding, or null
 };
 
 hipError_t launch_prefill(int layout, int xtype, int stype, bool zp, const PrefillArgs& a, hipStream_t stream,

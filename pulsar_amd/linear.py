@@ -92,8 +92,9 @@ class W4A16Linear(torch.nn.Module):
             x2 = x2.contiguous()
         y = ops.gemm_w4a16_gptq(x2, self.weight_marlin, self.scales, self.qzeros, self.perm, self.group_size)
         if self.bias is not None:
-            # at::linear's bias (Qwen2's q, k, v): summed with the rounded GEMM output in
-            # fp32 and rounded once to x's dtype
+            # at::linear's bias (Qwen2's q, k, v): summed in fp32 with the GEMM output,
+            # which is already rounded to x's dtype, and rounded again (at::linear
+            # rounds x @ W^T + b once)
             y.add_(self.bias)
         return y.reshape(*lead, self.out_features)
 

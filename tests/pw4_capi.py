@@ -34,6 +34,7 @@ def declare(L: ctypes.CDLL) -> ctypes.CDLL:
         "pw4_repack_gptq": (INT, [P, P, I64, I64, P, P]),
         "pw4_abi_version": (INT, []),
         "pw4_time_next_kernel": (INT, [P, P]),
+        "pw4_observe_next_call": (INT, [P]),
         "pw4_gemm_w4a16_marlin_noalloc": (INT, [P, INT, P, P, INT, P, P, P, I64, I64, I64, I64, I64, P]),
     }
     for name, (res, args) in sig.items():
@@ -89,6 +90,60 @@ class Hip:
 
     def sync(self) -> None:
         self._ok(self.lib.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+    # ---- streams and graph capture (for the capture tests) ----------------
+    CAPTURE_GLOBAL = 0
+
+    def _declare_graph_calls(self) -> None:
+        L = self.lib
+        if getattr(self, "_graph_calls", False):
+            return
+        L.hipStreamCreate.argtypes = [ctypes.POINTER(P)]
+        L.hipStreamDestroy.argtypes = [P]
+        L.hipStreamSynchronize.argtypes = [P]
+        L.hipStreamBeginCapture.argtypes = [P, INT]
+        L.hipStreamEndCapture.argtypes = [P, ctypes.POINTER(P)]
+        L.hipGraphGetNodes.argtypes = [P, P, ctypes.POINTER(SZ)]
+        L.hipGraphInstantiate.argtypes = [ctypes.POINTER(P), P, P, P, SZ]
+        L.hipGraphLaunch.argtypes = [P, P]
+        L.hipGraphExecDestroy.argtypes = [P]
+        L.hipGraphDestroy.argtypes = [P]
+        for f in (L.hipStreamCreate, L.hipStreamDestroy, L.hipStreamSynchronize, L.hipStreamBeginCapture,
+                  L.hipStreamEndCapture, L.hipGraphGetNodes, L.hipGraphInstantiate, L.hipGraphLaunch,
+                  L.hipGraphExecDestroy, L.hipGraphDestroy):
+            f.restype = INT
+        self._graph_calls = True
+
+    def stream(self) -> int:
+        self._declare_graph_calls()
+        s = P()
+        self._ok(self.lib.hipStreamCreate(ctypes.byref(s)), "hipStreamCreate")
+        return s.value
+
+    def stream_sync(self, s: int) -> None:
+        self._ok(self.lib.hipStreamSynchronize(s), "hipStreamSynchronize")
+
+    def capture(self, s: int, record) -> tuple[int, int]:
+        """Capture what record(s) launches on stream s; returns (graph, node count)."""
+        self._declare_graph_calls()
+        self._ok(self.lib.hipStreamBeginCapture(s, self.CAPTURE_GLOBAL), "hipStreamBeginCapture")
+        try:
+            record(s)
+        finally:
+            g = P()
+            rc = self.lib.hipStreamEndCapture(s, ctypes.byref(g))
+        self._ok(rc, "hipStreamEndCapture")
+        n = SZ(0)
+        self._ok(self.lib.hipGraphGetNodes(g, None, ctypes.byref(n)), "hipGraphGetNodes")
+        return g.value, n.value
+
+    def instantiate(self, g: int) -> int:
+        ge = P()
+        self._ok(self.lib.hipGraphInstantiate(ctypes.byref(ge), g, None, None, 0), "hipGraphInstantiate")
+        return ge.value
+
+    def launch_graph(self, ge: int, s: int) -> None:
+        self._ok(self.lib.hipGraphLaunch(ge, s), "hipGraphLaunch")
 
     def free_all(self) -> None:
         self.sync()

@@ -80,7 +80,7 @@ def test_act_order_llama70b(layer, m):
     print(f"act-order 70B {layer} m={m}: {r}")
 
 
-@pytest.mark.parametrize("layer", ["qkv", "down"])
+@pytest.mark.parametrize("layer", list(LLAMA70B))
 @pytest.mark.parametrize("m", [1, 16, 2048])
 def test_act_order_llama70b_bf16(layer, m):
     """Config 4 with bf16 activations (the reference engine's dtype): asymmetric int4,
@@ -98,7 +98,7 @@ def test_act_order_llama70b_bf16(layer, m):
     print(f"act-order 70B bf16 {layer} m={m}: {r}")
 
 
-@pytest.mark.parametrize("layer", ["o", "gate_up", "down"])
+@pytest.mark.parametrize("layer", list(LLAMA8B))
 def test_output_checksum_prefill(layer):
     """Column sums of y over ALL rows against the oracle: sum_m y[m, :] equals
     (sum_m x[m, :]) @ W^T up to fp16 output rounding of each term."""

@@ -95,3 +95,108 @@ def test_noalloc_rejects_plans_beyond_the_scratch(env):
     # forced K slices whose partials do not fit are rejected too (automatic plans run unsplit)
     assert lib.pw4_gemm_w4a16_marlin_noalloc(x, DTYPE_F16, wm, sc, DTYPE_F16, None, None, y, m, n, k, G, 16,
                                              None) == -3
+
+
+# ---- under HIP graph capture ------------------------------------------------
+# (M, N, K, num_splits, act_order): every kind of scratch use, as above
+CAPTURE_CALLS = [
+    (16, 2048, 14336, 0, False),   # exchange-tree slots in the zero region
+    (4, 512, 4096, 3, False),      # forced K slices: counters + partials
+    (300, 1040, 2048, 4, False),   # prefill K-slice partials + combine
+    (8, 1024, 8192, 0, True),      # act-order copy of x
+]
+
+
+def _capture_check() -> None:
+    """Run in a fresh process, so that its first no-alloc call is made while a
+    stream is capturing.  Checks, bit for bit against the workspace entry
+    point: replays of graphs captured before any eager no-alloc call (the
+    zero-region fill recorded once per graph, ahead of its first call), an
+    eager call after them, and a graph captured after that (no fill)."""
+    lib = declare(pulsar_amd.capi())
+    hip = Hip()
+    cases = []
+    for i, (m, n, k, splits, act) in enumerate(CAPTURE_CALLS):
+        p = O.make_problem(m, n, k, G, seed=120 + i, symmetric=not act, act_order=act)
+        wm, sc, sdt, qz, perm = _operands(lib, hip, p)
+        x = hip.upload(p.x16)
+        need = lib.pw4_gemm_w4a16_marlin_workspace_size(m, n, k, G, int(act), splits)
+        ws = hip.malloc(max(need, 1))
+        hip.memset(ws, 0, max(need, 1))
+        y_ws = hip.malloc(m * n * 2)
+        assert lib.pw4_gemm_w4a16_marlin(x, DTYPE_F16, wm, sc, sdt, qz, perm, y_ws, m, n, k, G, splits, ws, need,
+                                         None) == 0
+        want = hip.download(y_ws, (m, n), np.uint16)
+        cases.append(dict(args=(x, DTYPE_F16, wm, sc, sdt, qz, perm), shape=(m, n, k, splits),
+                          y=hip.malloc(m * n * 2), want=want))
+
+    def call(case, s):
+        x, xd, wm, sc, sdt, qz, perm = case["args"]
+        m, n, k, splits = case["shape"]
+        rc = lib.pw4_gemm_w4a16_marlin_noalloc(x, xd, wm, sc, sdt, qz, perm, case["y"], m, n, k, G, splits, s)
+        assert rc == 0, (lib.pw4_status_string(rc), lib.pw4_last_hip_error())
+
+    def check(which, tag):
+        for i in which:
+            c = cases[i]
+            m, n = c["shape"][:2]
+            got = hip.download(c["y"], (m, n), np.uint16)
+            assert np.array_equal(got, c["want"]), f"{tag}: call {i} {c['shape']} differs from the workspace entry point"
+
+    def replay(ge, s, which, tag, times):
+        for r in range(times):
+            for i in which:
+                m, n = cases[i]["shape"][:2]
+                hip.memset(cases[i]["y"], 0xFF, m * n * 2)
+            hip.sync()
+            hip.launch_graph(ge, s)
+            hip.stream_sync(s)
+            check(which, f"{tag} replay {r}")
+
+    s = hip.stream()
+    # cold: no no-alloc call has run in this process
+    _, n1 = hip.capture(s, lambda st: call(cases[0], st))
+    g3, n3 = hip.capture(s, lambda st: [call(cases[0], st) for _ in range(3)])
+    # one fill node per graph, however many calls it holds
+    assert n3 == 3 * n1 - 2, f"cold graphs: {n1} nodes for one call, {n3} for three (one fill expected in each)"
+    gall, _ = hip.capture(s, lambda st: [call(c, st) for c in cases])
+    e3, eall = hip.instantiate(g3), hip.instantiate(gall)
+    replay(eall, s, range(len(cases)), "cold graph of every kind", 3)
+    replay(e3, s, [0], "cold graph of three calls", 2)
+    # an eager call clears the region for good ...
+    call(cases[1], s)
+    hip.stream_sync(s)
+    check([1], "eager call after the cold graphs")
+    # ... so a graph captured after it records no fill
+    g3w, n3w = hip.capture(s, lambda st: [call(cases[0], st) for _ in range(3)])
+    assert n3w == n3 - 1, f"warm graph of three calls: {n3w} nodes against {n3} with the fill"
+    e3w = hip.instantiate(g3w)
+    replay(e3w, s, [0], "warm graph", 2)
+    replay(eall, s, range(len(cases)), "cold graph after the eager call", 2)
+    # a stream of the current device is required; the default stream is one
+    hip.sync()
+    hip.free_all()
+    print("capture check ok", flush=True)
+
+
+def test_noalloc_under_graph_capture():
+    """The first no-alloc call of a process made under stream capture, then
+    replays, eager calls and a warm capture (see _capture_check); run in a
+    child process so that the call really is the process's first."""
+    import os
+    import subprocess
+    import sys
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([here, os.path.dirname(here), env.get("PYTHONPATH", "")])
+    r = subprocess.run([sys.executable, "-u", os.path.abspath(__file__), "capture"], env=env, capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode == 0 and "capture check ok" in r.stdout, f"child failed ({r.returncode}):\n{r.stdout}\n{r.stderr}"
+
+
+if __name__ == "__main__":
+    import sys as _sys
+
+    if len(_sys.argv) > 1 and _sys.argv[1] == "capture":
+        _capture_check()
