@@ -47,16 +47,22 @@ int x_dtype_code(const at::Tensor& x) { return x.scalar_type() == at::kBFloat16 
 //  * a buffer is never freed.  When a call needs more, the smaller buffer is
 //    retired but kept alive until the process exits, so a graph that captured
 //    its address still replays into valid memory that nothing else uses;
-//  * a buffer allocated while the stream captures is zeroed by a fill node of
-//    the graph (at::zeros records one), so a replay zeroes it before the GEMM.
-//    That fill never ran eagerly: the next eager call on the stream zeroes
-//    the buffer first, and the next capture records a fill of its own;
+//  * only the zero region (the first PW4_ZERO_REGION_BYTES) has to be zero;
+//    the rest is scratch that every call writes before it reads it;
+//  * a buffer allocated while the stream captures has its zero region
+//    cleared by a fill node of the graph (zero_() records a kernel), so a
+//    replay clears it before the GEMM.  The fill is recorded once per
+//    capture: the calls after it in the graph find the region as the earlier
+//    ones left it, zero.  Such a fill never ran eagerly, so the next eager
+//    call on the stream clears the region first, and a later capture records
+//    a fill of its own until then;
 //  * graphs captured on one stream share that stream's buffer, so they are
 //    replayed in order (on one stream, or synchronised), like the calls of a
 //    stream.
 struct StreamWorkspace {
     at::Tensor buf;
     bool zeroed_eagerly = true;  // false until a buffer allocated under capture is zeroed outside it
+    unsigned long long fill_capture = 0;  // capture id whose graph already holds the fill (0: none)
 };
 
 at::Tensor workspace(size_t bytes, const at::Tensor& like) {
@@ -66,20 +72,25 @@ at::Tensor workspace(size_t bytes, const at::Tensor& like) {
     static std::vector<at::Tensor> retired;
     const auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA();
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    TORCH_CHECK(hipStreamIsCapturing(stream.stream(), &cs) == hipSuccess,
-                "W4A16 workspace: hipStreamIsCapturing failed");
-    const bool capturing = cs != hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    TORCH_CHECK(hipStreamGetCaptureInfo(stream.stream(), &cs, &cid) == hipSuccess,
+                "W4A16 workspace: hipStreamGetCaptureInfo failed");
+    const bool capturing = cs == hipStreamCaptureStatusActive;
     const std::pair<int64_t, int64_t> key{like.device().index(), (int64_t)stream.id()};
     std::lock_guard<std::mutex> lock(mu);
     StreamWorkspace& w = cache[key];
+    auto clear_zero_region = [&]() {
+        w.buf.narrow(0, 0, std::min<int64_t>(w.buf.numel(), (int64_t)PW4_ZERO_REGION_BYTES)).zero_();
+        w.zeroed_eagerly = !capturing;
+        w.fill_capture = capturing ? cid : 0;
+    };
     if (!w.buf.defined() || (size_t)w.buf.numel() < bytes) {
         const size_t grow = w.buf.defined() ? std::max(bytes, (size_t)w.buf.numel() * 2) : bytes;
         if (w.buf.defined()) retired.push_back(std::move(w.buf));
-        w.buf = at::zeros({(int64_t)grow}, like.options().dtype(at::kByte));
-        w.zeroed_eagerly = !capturing;
-    } else if (!w.zeroed_eagerly) {
-        w.buf.zero_();  // eagerly, or as a fill node of this capture too
-        w.zeroed_eagerly = !capturing;
+        w.buf = at::empty({(int64_t)grow}, like.options().dtype(at::kByte));
+        clear_zero_region();
+    } else if (!w.zeroed_eagerly && !(capturing && w.fill_capture == cid)) {
+        clear_zero_region();  // eagerly, or as a fill node of this capture
     }
     return w.buf;
 }

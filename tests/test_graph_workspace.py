@@ -152,3 +152,71 @@ def test_two_graphs_on_one_stream_growing_workspace():
             e1 = _gemm(x1, w)
         s.synchronize()
         assert torch.equal(e1, ref1)
+
+
+def _graph_nodes(g) -> int:
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipGraphGetNodes.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_size_t)]
+    hip.hipGraphGetNodes.restype = ctypes.c_int
+    n = ctypes.c_size_t(0)
+    assert hip.hipGraphGetNodes(ctypes.c_void_p(g.raw_cuda_graph()), None, ctypes.byref(n)) == 0
+    return n.value
+
+
+def _fresh_stream():
+    """A stream the shim has never seen (its workspace cache is keyed by stream)."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipStreamCreate.restype = ctypes.c_int
+    p = ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(p)) == 0
+    return torch.cuda.ExternalStream(p.value)
+
+
+def test_one_zero_fill_per_capture():
+    """Several split calls captured on a stream with no eager call before: the
+    graph holds ONE fill of the workspace's zero region (not one per call, not
+    of the whole buffer), and its replays and the eager calls between them are
+    exact.  Node counts are compared with the same calls captured on a stream
+    whose workspace an eager call has already cleared (no fill at all)."""
+    down = _weights(14336, 4096, seed=12)
+    o = _weights(4096, 4096, seed=13)
+    x8, x256 = _x(8, 14336, seed=14), _x(256, 4096, seed=15)
+    sm = o[1].float()
+
+    # the largest workspace first: a buffer that grows inside the capture is a
+    # new allocation, which needs (and gets) a fill of its own
+    def calls():
+        return [ops.gemm_w4a16_marlin_split(x256, o[0], sm, G, 4),  # K-slice partials + combine
+                _gemm(x8, down),                                   # exchange-tree decode
+                _gemm(x8, down)]
+
+    refs = [t.clone() for t in calls()]
+    warm = _fresh_stream()
+    with torch.cuda.stream(warm):
+        calls()
+    warm.synchronize()
+    gw = torch.cuda.CUDAGraph(keep_graph=True)
+    with torch.cuda.graph(gw, stream=warm):
+        calls()
+    cold = _fresh_stream()
+    gc = torch.cuda.CUDAGraph(keep_graph=True)
+    with torch.cuda.graph(gc, stream=cold):
+        outs = calls()
+    assert _graph_nodes(gc) == _graph_nodes(gw) + 1, (_graph_nodes(gc), _graph_nodes(gw))
+    for _ in range(3):
+        for t in outs:
+            t.zero_()
+        gc.replay()
+        torch.cuda.synchronize()
+        for t, r in zip(outs, refs):
+            assert torch.equal(t, r)
+        with torch.cuda.stream(cold):
+            eager = calls()
+        cold.synchronize()
+        for t, r in zip(eager, refs):
+            assert torch.equal(t, r)
