@@ -86,6 +86,19 @@ int pw4_time_next_kernel(void* start_event, void* stop_event);
  * arguments, so it never outlives that call; NULL disarms. */
 int pw4_observe_next_call(float* y32);
 
+/* Diagnostic, no counterpart in the reference (it is for tests and tuning):
+ * writes into buf (len bytes, NUL-terminated) the plan a GEMM call with these
+ * arguments would run, e.g. "decode nb=16 wps=256 splits=1 tree=0 win=0 ring=4
+ * mt=1" or "prefill256 rows=128 splits=2 exact=1".  layout: PW4_LAYOUT_CT
+ * (pw4_gemm_w4a16) or PW4_LAYOUT_MARLIN (pw4_gemm_w4a16_marlin; with silu
+ * nonzero pw4_gemm_w4a16_silu_mul).  Launches nothing.  The plan depends on
+ * the current device's compute-unit count (256 assumed when no device
+ * answers).  PW4_ERR_ARG when buf is too small. */
+#define PW4_LAYOUT_CT 0
+#define PW4_LAYOUT_MARLIN 1
+int pw4_plan_describe(int layout, int x_dtype, int scale_dtype, int has_zp, int has_perm, int silu, int64_t M,
+                      int64_t N, int64_t K, int64_t group_size, int64_t num_splits, char* buf, size_t len);
+
 /* ABI version of this header: bumped on any incompatible change. */
 int pw4_abi_version(void);
 #define PW4_ABI_VERSION 2

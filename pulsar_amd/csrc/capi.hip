@@ -156,7 +156,11 @@ int decode_win_mode() {
 //     8192 x 10240 at M = 2048 343 us on 2 K slices against 372 on the 3
 //     the model picked without it, at M = 4096 579 unsplit against 666 on 2);
 //   * K slices add their fp32 partials' round trip, s * M * N * 8 bytes at
-//     8 TB/s, plus 1 us for the combine launch.
+//     6 TB/s, plus 1 us for the combine launch.  (At 8 TB/s the model took 2
+//     slices for Llama-3-8B o at M = 1024 and 2048 and gate_up at M = 256,
+//     measured 1-8% slower than its picks at 6 TB/s -- o M = 2048 unsplit 74-82
+//     us against 80-84 on 2 slices; every other 8B and 70B pick at M = 256..4096
+//     is the same at both rates and the measured fastest, within 1 us.)
 // fp16 activations with exact scaling use 128-row tiles only: on the same
 // sweep the model's 128-row picks are within 0.6% of the per-shape best (8367
 // against 8322 us); 256-row tiles were ahead on down_proj of 70B alone, by 1-3%.
@@ -175,8 +179,9 @@ bool prefill_exact_enabled() {
 
 // only128: 128-row tiles only (exact scaling); max_splits: the most K slices
 // the plan may use.
-Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, bool only128, int64_t max_splits) {
-    constexpr double kChunk256 = 1.6, kChunk128Solo = 1.1, kChunk128Pair = 1.6, kPartialBps = 8.0e12,
+Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, bool only128, int64_t max_splits,
+                               double* cost_us = nullptr) {
+    constexpr double kChunk256 = 1.6, kChunk128Solo = 1.1, kChunk128Pair = 1.6, kPartialBps = 6.0e12,
                      kCombineUs = 1.0;
     Prefill256Plan best{256, 1};
     double best_us = 0.0;
@@ -210,7 +215,28 @@ Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, b
             }
         }
     }
+    if (cost_us) *cost_us = best_us;
     return best;
+}
+
+// Decode kernel or 128-row prefill tile at M = 28..32 (MARLIN layout).  There
+// the decode kernel runs two 16-row tiles per wave and K slices of the
+// activations, and streams a layer's weights at about 1.6 TB/s whatever its
+// shape; the prefill tile's time follows the plan model above, which reads
+// 1.2-1.45x low at these M (measured on MI355X, us, decode / prefill tile:
+// Llama-3-70B gate_up 8192 x 57344 at M = 28 140 / 131 and M = 32 145 / 133;
+// every other 8B and 70B layer faster on the decode kernel at M = 17..32, e.g.
+// 70B qkv M = 32 26.5 / 31.5, 70B down 69 / 78, 8B gate_up 36 / 44).  Below
+// M = 28 the decode kernel was faster on every layer (70B gate_up M = 24 113 /
+// 131).
+bool prefer_prefill_tile(int xt, int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
+    constexpr double kDecodeBps = 1.6e12, kModelLow = 1.25;
+    if (M < 28 || !prefill256_ok(LAYOUT_MARLIN, xt, N, K, G)) return false;
+    double prefill_us = 0.0;
+    plan_prefill256(M, N, ceil_div(round_up(K, kMarlinBK), 64), cus, xt == X_F16 && prefill_exact_enabled(), 8,
+                    &prefill_us);
+    const double decode_us = (double)N * (double)K / 2.0 / kDecodeBps * 1e6;
+    return kModelLow * prefill_us < decode_us;
 }
 
 struct Plan {
@@ -259,7 +285,12 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
     // M = 33 and 64 / prefill at M = 65: 8B gate_up 58 and 136 / 35, down 36
     // and 145 / 36, 70B gate_up 218 and 852 / 114, down 210 and 1031 / 74).
     bool decode_ok = M <= 32 && G >= 16 && (G & (G - 1)) == 0;
-    if (decode_mode_override() == 0) decode_ok = false;
+    const int decode_mode = decode_mode_override();
+    if (decode_mode == 0) decode_ok = false;
+    if (decode_ok && decode_mode != 1 && !forced && layout == LAYOUT_MARLIN &&
+        prefer_prefill_tile(x_dtype == PW4_DTYPE_BF16 ? X_BF16 : X_F16, M, N, K, G, cus)) {
+        decode_ok = false;
+    }
     if (decode_ok) {
         DecodeConfig dc{};
         dc.mt = M <= 16 ? 1 : 2;
@@ -749,6 +780,30 @@ int pw4_time_next_kernel(void* start_event, void* stop_event) {
 int pw4_observe_next_call(float* y32) {
     pw4::g_armed_events.y32 = y32;
     return PW4_OK;
+}
+
+int pw4_plan_describe(int layout, int x_dtype, int scale_dtype, int has_zp, int has_perm, int silu, int64_t M,
+                      int64_t N, int64_t K, int64_t group_size, int64_t num_splits, char* buf, size_t len) {
+    if (layout != PW4_LAYOUT_CT && layout != PW4_LAYOUT_MARLIN) return PW4_ERR_ARG;
+    int rc = check_common(M, N, K, group_size, x_dtype);
+    if (rc != PW4_OK) return rc;
+    if (num_splits < 0 || buf == nullptr || len == 0) return PW4_ERR_ARG;
+    if (scale_dtype != PW4_DTYPE_F32 && scale_dtype != PW4_DTYPE_F16) return PW4_ERR_ARG;
+    if (M == 0 || N == 0) return PW4_ERR_SHAPE;
+    const int lay = layout == PW4_LAYOUT_MARLIN ? LAYOUT_MARLIN : LAYOUT_CT;
+    const Plan p = make_plan(lay, x_dtype, scale_dtype == PW4_DTYPE_F32 ? S_F32 : S_F16, has_zp != 0, M, N, K,
+                             group_size, has_perm != 0, num_splits, silu != 0);
+    int n;
+    if (p.decode) {
+        n = std::snprintf(buf, len, "decode nb=%d wps=%d splits=%d tree=%d win=%d ring=%d mt=%d", p.dc.nb, p.dc.wps,
+                          p.dc.splits, p.tree ? 1 : 0, p.dc.kwin > 0 ? 1 : 0, p.dc.ring, p.dc.mt);
+    } else if (p.p256) {
+        n = std::snprintf(buf, len, "prefill256 rows=%d splits=%d exact=%d%s", p.p_tile_rows, p.p_splits,
+                          p.p_exact ? 1 : 0, p.repack_bytes ? " repack" : "");
+    } else {
+        n = std::snprintf(buf, len, "prefill128 splits=%d", p.p_splits);
+    }
+    return n < 0 || (size_t)n >= len ? PW4_ERR_ARG : PW4_OK;
 }
 
 int pw4_abi_version(void) { return PW4_ABI_VERSION; }

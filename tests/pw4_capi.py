@@ -35,6 +35,7 @@ def declare(L: ctypes.CDLL) -> ctypes.CDLL:
         "pw4_abi_version": (INT, []),
         "pw4_time_next_kernel": (INT, [P, P]),
         "pw4_observe_next_call": (INT, [P]),
+        "pw4_plan_describe": (INT, [INT, INT, INT, INT, INT, INT, I64, I64, I64, I64, I64, ctypes.c_char_p, SZ]),
         "pw4_gemm_w4a16_marlin_noalloc": (INT, [P, INT, P, P, INT, P, P, P, I64, I64, I64, I64, I64, P]),
     }
     for name, (res, args) in sig.items():

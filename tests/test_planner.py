@@ -1,0 +1,117 @@
+"""The plans the library picks for the BASELINE layers, read through pw4_plan_describe
+(host logic only: nothing launches).  Each pinned choice is the measured-faster plan on
+MI355X (256 CUs; kernel or call times in the comments, us):
+
+* M = 28..32 on the decode kernel, except Llama-3-70B gate_up (8192 x 57344), which is
+  faster on the 128-row prefill tile (M = 28: 140 decode / 131 prefill; M = 32: 145 /
+  133); at M = 24 the decode kernel still wins there (113 / 131), and at M = 32 on every
+  other 8B and 70B layer (70B qkv 26.5 / 31.5, 70B down 69 / 78, 8B gate_up 36 / 44).
+* Prefill K slices: Llama-3-8B o unsplit at M = 2048 (74-82 against 80-84 on 2 slices),
+  2 slices at M = 1024 (51 against 52 on 4), gate_up unsplit at M = 256 (73-76 against
+  76-78 on 2), and the splits of the other layers as measured fastest.
+"""
+
+import ctypes
+import os
+
+import pytest
+
+import pulsar_amd
+from pw4_capi import DTYPE_BF16, DTYPE_F16, declare
+
+LAYOUT_CT, LAYOUT_MARLIN = 0, 1
+G = 128
+L8 = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 28672), "down": (14336, 4096)}
+L70 = {"qkv": (8192, 10240), "gate_up": (8192, 57344), "down": (28672, 8192)}
+OVERRIDES = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS", "PW4_PREFILL_EXACT", "PW4_PREFILL_TILE", "PW4_DECODE",
+             "PW4_DECODE_NB", "PW4_DECODE_SPLITS", "PW4_DECODE_WPS", "PW4_DECODE_WIN")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    saved = {k: os.environ.pop(k) for k in OVERRIDES if k in os.environ}
+    yield declare(pulsar_amd.capi())
+    os.environ.update(saved)
+
+
+def plan(lib, m, k, n, dtype=DTYPE_F16, layout=LAYOUT_MARLIN, zp=0, perm=0, silu=0, splits=0):
+    buf = ctypes.create_string_buffer(160)
+    rc = lib.pw4_plan_describe(layout, dtype, DTYPE_F16, zp, perm, silu, m, n, k, G, splits, buf, len(buf))
+    assert rc == 0, rc
+    return buf.value.decode()
+
+
+@pytest.mark.parametrize("m", [28, 32])
+@pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_BF16])
+def test_70b_gate_up_takes_the_prefill_tile_from_m28(lib, m, dtype):
+    k, n = L70["gate_up"]
+    assert plan(lib, m, k, n, dtype).startswith("prefill256"), plan(lib, m, k, n, dtype)
+    # act-order with zero points (config 4) plans the same way
+    assert plan(lib, m, k, n, dtype, zp=1, perm=1).startswith("prefill256")
+
+
+@pytest.mark.parametrize("m", [1, 16, 17, 24])
+def test_70b_gate_up_decode_below_m28(lib, m):
+    k, n = L70["gate_up"]
+    assert plan(lib, m, k, n).startswith("decode"), plan(lib, m, k, n)
+
+
+@pytest.mark.parametrize("layer", ["8b_qkv", "8b_o", "8b_gate_up", "8b_down", "70b_qkv", "70b_down"])
+@pytest.mark.parametrize("m", [1, 16, 28, 32])
+def test_other_layers_decode_up_to_m32(lib, layer, m):
+    model, name = layer.split("_", 1)
+    k, n = (L8 if model == "8b" else L70)[name]
+    assert plan(lib, m, k, n).startswith("decode"), (layer, m, plan(lib, m, k, n))
+
+
+def test_m33_leaves_the_decode_kernel(lib):
+    k, n = L8["down"]
+    assert plan(lib, 33, k, n).startswith("prefill256")
+
+
+def test_forced_splits_keep_the_decode_kernel(lib):
+    # gemm_w4a16_marlin_split at decode sizes: the reference's split path, on the decode kernel
+    # (8 slices: a 32-row slice of K / 8 fits the decode kernel's LDS, K / 4 does not)
+    k, n = L70["gate_up"]
+    assert plan(lib, 32, k, n, splits=8).startswith("decode"), plan(lib, 32, k, n, splits=8)
+
+
+@pytest.mark.parametrize("layer,m,want", [
+    ("o", 2048, "prefill256 rows=128 splits=1 exact=1"),
+    ("o", 1024, "prefill256 rows=128 splits=2 exact=1"),
+    ("o", 256, "prefill256 rows=128 splits=8 exact=1"),
+    ("gate_up", 256, "prefill256 rows=128 splits=1 exact=1"),
+    ("gate_up", 4096, "prefill256 rows=128 splits=1 exact=1"),
+    ("qkv", 1024, "prefill256 rows=128 splits=2 exact=1"),
+    ("qkv", 4096, "prefill256 rows=128 splits=1 exact=1"),
+    ("down", 256, "prefill256 rows=128 splits=8 exact=1"),
+    ("down", 1024, "prefill256 rows=128 splits=4 exact=1"),
+    ("down", 2048, "prefill256 rows=128 splits=2 exact=1"),
+    ("down", 4096, "prefill256 rows=128 splits=1 exact=1"),
+])
+def test_prefill_splits_8b(lib, layer, m, want):
+    k, n = L8[layer]
+    assert plan(lib, m, k, n) == want
+
+
+@pytest.mark.parametrize("layer,m,want", [
+    ("qkv", 256, "splits=6"), ("qkv", 1024, "splits=3"), ("qkv", 2048, "splits=2"), ("qkv", 4096, "splits=1"),
+    ("gate_up", 1024, "splits=1"), ("down", 256, "splits=8"), ("down", 1024, "splits=2"), ("down", 2048, "splits=1"),
+])
+def test_prefill_splits_70b(lib, layer, m, want):
+    k, n = L70[layer]
+    assert want in plan(lib, m, k, n), plan(lib, m, k, n)
+
+
+def test_ct_layout_repacks_past_the_decode_range(lib):
+    k, n = L8["o"]
+    assert plan(lib, 16, k, n, layout=LAYOUT_CT).startswith("decode")
+    assert plan(lib, 64, k, n, layout=LAYOUT_CT).endswith("repack")
+
+
+def test_describe_rejects_bad_arguments(lib):
+    buf = ctypes.create_string_buffer(8)
+    assert lib.pw4_plan_describe(LAYOUT_MARLIN, DTYPE_F16, DTYPE_F16, 0, 0, 0, 1, 4096, 4096, G, 0, buf, 8) == -1
+    big = ctypes.create_string_buffer(160)
+    assert lib.pw4_plan_describe(7, DTYPE_F16, DTYPE_F16, 0, 0, 0, 1, 4096, 4096, G, 0, big, 160) == -1
+    assert lib.pw4_plan_describe(LAYOUT_MARLIN, DTYPE_F16, DTYPE_F16, 0, 0, 0, 1, 4096, 4100, G, 0, big, 160) == -2
