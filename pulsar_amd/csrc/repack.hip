@@ -151,8 +151,12 @@ __global__ __launch_bounds__(kRepackThreads) void repack_gptq_kernel(const uint3
 // nibble).  A thread takes 4 adjacent columns of one 32-K tile: each 8-entry run
 // of the permutation is one 16-byte LDS read shared by the tile's threads, and
 // each source row one 16-byte read for the 4 columns.  grid: Npad/NB.
+// Staging reads 4 adjacent columns of a row per 16-byte load (VEC: N % 4 == 0
+// and 16-byte aligned qweight; otherwise word by word), 8 loads in flight per
+// thread, and the permutation 4 entries per 16-byte load (K % 4 == 0 always:
+// K % 8 == 0 on this path).
 constexpr int kPermThreads = 512;
-template <int NB>
+template <int NB, bool VEC>
 __global__ __launch_bounds__(kPermThreads) void repack_gptq_perm_kernel(const uint32_t* __restrict__ qweight,
                                                                         const int32_t* __restrict__ perm,
                                                                         uint32_t* __restrict__ wm, int N, int K,
@@ -167,60 +171,97 @@ __global__ __launch_bounds__(kPermThreads) void repack_gptq_perm_kernel(const ui
     // staging, kStage loads in flight per thread before their LDS stores (a
     // store right behind its load would make every step a memory round trip)
     constexpr int kStage = 8;
-    for (int i0 = threadIdx.x; i0 < k8 * NB; i0 += kPermThreads * kStage) {
-        uint32_t v[kStage];
+    constexpr int kQuadsPerRow = NB / 4;
+    const u32x4 pad4 = u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};  // padding: nibble 8
+    for (int i0 = threadIdx.x; i0 < k8 * kQuadsPerRow; i0 += kPermThreads * kStage) {
+        u32x4 v[kStage];
 #pragma unroll
         for (int q = 0; q < kStage; ++q) {
             const int i = i0 + q * kPermThreads;
-            const int r = i / NB, c = i % NB;
-            v[q] = (i < k8 * NB && n0 + c < N) ? qweight[(int64_t)r * N + n0 + c] : 0x88888888u;  // padding: nibble 8
+            const int r = i / kQuadsPerRow, c = (i % kQuadsPerRow) * 4;
+            const uint32_t* src = qweight + (int64_t)r * N + n0 + c;
+            v[q] = pad4;
+            if (i < k8 * kQuadsPerRow) {
+                if (VEC && n0 + c + 3 < N) {
+                    v[q] = *reinterpret_cast<const u32x4*>(src);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n0 + c + e < N) v[q][e] = src[e];
+                }
+            }
         }
 #pragma unroll
         for (int q = 0; q < kStage; ++q) {
             const int i = i0 + q * kPermThreads;
-            if (i < k8 * NB) sq[i] = v[q];
+            if (i < k8 * kQuadsPerRow) *reinterpret_cast<u32x4*>(sq + (int64_t)i * 4) = v[q];
         }
     }
     // padding rows (k >= K) point at row 0 and are masked below
-    for (int k0 = threadIdx.x; k0 < kpad; k0 += kPermThreads * kStage) {
-        int v[kStage];
+    for (int k0 = threadIdx.x * 4; k0 < kpad; k0 += kPermThreads * 4 * kStage) {
+        u32x4 v[kStage];
 #pragma unroll
         for (int q = 0; q < kStage; ++q) {
-            const int k = k0 + q * kPermThreads;
-            v[q] = k < K ? min(max(perm[k], 0), K - 1) : 0;  // clamped: a bad perm cannot fault
+            const int k = k0 + q * kPermThreads * 4;
+            v[q] = u32x4{0u, 0u, 0u, 0u};
+            if (k < K) {  // K % 4 == 0: whole vectors
+                if constexpr (VEC) {
+                    v[q] = *reinterpret_cast<const u32x4*>(perm + k);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[q][e] = (uint32_t)perm[k + e];
+                }
+            }
         }
 #pragma unroll
         for (int q = 0; q < kStage; ++q) {
-            const int k = k0 + q * kPermThreads;
-            if (k < kpad) sp[k] = (uint16_t)v[q];
+            const int k = k0 + q * kPermThreads * 4;
+            if (k < kpad) {
+                uint32_t p2[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    // clamped: a bad perm cannot fault
+                    const uint32_t a = (uint32_t)min(max((int)v[q][2 * h], 0), K - 1);
+                    const uint32_t b = (uint32_t)min(max((int)v[q][2 * h + 1], 0), K - 1);
+                    p2[h] = a | (b << 16);
+                }
+                *reinterpret_cast<u32x2*>(sp + k) = u32x2{p2[0], p2[1]};
+            }
         }
     }
     __syncthreads();
     constexpr int kQuads = NB / 4;  // threads per tile
     const int ktiles = nchunks * 2;
+    // Each gathered nibble goes straight to its MARLIN place: K offset 8j + e of
+    // the tile (run j, entry e) is nibble j + 4 (e % 2) of word e / 2 -- the
+    // word transpose_tile_bytes would build from source run j's byte e / 2.
     for (int i = threadIdx.x; i < ktiles * kQuads; i += kPermThreads) {
         const int t = i / kQuads, c0 = (i % kQuads) * 4;
-        uint32_t src[4][4];  // [column][32-bit run j]
+        uint32_t out[4][4] = {};  // [column q][MARLIN word tg]
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int kb = t * 32 + j * 8;
+            if (kb >= K) {  // padding rows (K % 8 == 0: whole runs): nibble 8
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int tg = 0; tg < 4; ++tg) out[q][tg] |= (8u << (4 * j)) | (8u << (4 * j + 16));
+                continue;
+            }
             const u32x4 pk = *reinterpret_cast<const u32x4*>(sp + kb);  // 8 permutation entries
-            uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int sk = (pk[e >> 1] >> (16 * (e & 1))) & 0xffff;
                 const u32x4 row = *reinterpret_cast<const u32x4*>(sq + (sk >> 3) * NB + c0);
                 const int sh = 4 * (sk & 7);
-                const bool pad = kb + e >= K;  // padding rows: nibble 8
 #pragma unroll
-                for (int q = 0; q < 4; ++q) w[q] |= (pad ? 8u : (row[q] >> sh) & 0xfu) << (4 * e);
+                for (int q = 0; q < 4; ++q) out[q][e >> 1] |= ((row[q] >> sh) & 0xfu) << (4 * j + 16 * (e & 1));
             }
-#pragma unroll
-            for (int q = 0; q < 4; ++q) src[q][j] = w[q];
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            *reinterpret_cast<u32x4*>(wm + marlin_offset(n0 + c0 + q, t, nchunks)) = transpose_tile_bytes(src[q]);
+            *reinterpret_cast<u32x4*>(wm + marlin_offset(n0 + c0 + q, t, nchunks)) =
+                u32x4{out[q][0], out[q][1], out[q][2], out[q][3]};
         }
     }
 }
@@ -313,7 +354,9 @@ template <int NB>
 hipError_t launch_repack_gptq_perm(const uint32_t* qweight, const int32_t* perm, uint32_t* wm, int N, int K,
                                    int npad, int kpad, size_t lds, hipStream_t stream, hipEvent_t start,
                                    hipEvent_t stop) {
-    const auto fn = repack_gptq_perm_kernel<NB>;
+    // 16-byte staging loads: 4-column quads of a row and 4-entry runs of perm aligned
+    const bool vec = N % 4 == 0 && ((reinterpret_cast<uintptr_t>(qweight) | reinterpret_cast<uintptr_t>(perm)) & 15) == 0;
+    const auto fn = vec ? repack_gptq_perm_kernel<NB, true> : repack_gptq_perm_kernel<NB, false>;
     if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;

@@ -26,13 +26,15 @@ def test_symmetric_gptq_equals_reference_repack(n, k):
 
 # The act-order repack stages a column block's source words and the permutation in LDS,
 # 4 to 64 columns wide by K and N: the shapes below take every width (K up to 28672),
-# ragged N and K tails.
+# ragged N and K tails; N % 4 != 0 (130, 66) takes the word-by-word staging path, the
+# others 16-byte staging loads.
 @pytest.mark.parametrize("n,k,g", [(256, 1024, 128), (136, 512, 64), (64, 256, 32), (128, 4096, 128),
                                    (200, 2112, 64), (14336, 4096, 128), (4096, 4096, 128),
                                    (1024, 4096, 128), (4096, 14336, 128), (512, 28672, 128), (16384, 4096, 128),
-                                   (2048, 4096, 128)])
+                                   (2048, 4096, 128), (130, 1024, 128), (66, 2048, 64)])
 def test_act_order_repack_bit_exact(n, k, g):
-    c = baseline_case(1, n, k, g, seed=3, symmetric=False, act_order=True)
+    # (the repack moves qweight only; int4 zero points exist for N % 8 == 0)
+    c = baseline_case(1, n, k, g, seed=3, symmetric=n % 8 != 0, act_order=True)
     g_idx = torch.from_numpy(c.g_idx).cuda()
     wm, perm = ops.repack_w4a16_gptq(c.qweight(), g_idx, g)
     want_perm = O.gidx_perm(c.g_idx, g)
