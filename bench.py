@@ -1047,6 +1047,10 @@ def main() -> int:
             "unit": "GB/s",
             "frac": None if achieved is None else round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": None if traffic is None else (
+                "not measured in this run: bytes_per_launch of profiles/decode_traffic.json, the committed "
+                "summary of two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE, calibrated against a "
+                "512 MiB copy) of `bench.py --pmc-workload decode` (profiles/decode_traffic.md)"),
             "mean_launch_us": None if mean_launch_us is None else round(mean_launch_us, 3),
             "timing": None if achieved is None else (
                 "achieved = mean algorithmic bytes / mean decode-kernel duration over single launches of "
