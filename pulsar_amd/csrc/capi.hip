@@ -111,6 +111,13 @@ int prefill_splits_override() {
     const int v = std::atoi(e);
     return (v >= 1 && v <= 64) ? v : 0;
 }
+// K halves of the 128-row tiles (1 or 2), for tuning sweeps; 0 = heuristic.
+int prefill_khalves_override() {
+    const char* e = plan_env("PW4_PREFILL_KHALVES");
+    if (!e) return 0;
+    const int v = std::atoi(e);
+    return (v == 1 || v == 2) ? v : 0;
+}
 
 // Decode kernel override for tuning sweeps: 0 keeps every M off the decode
 // kernel (prefill kernels only), 1 keeps M <= 32 on it; unset = heuristic.
@@ -164,9 +171,22 @@ int decode_win_mode() {
 // fp16 activations with exact scaling use 128-row tiles only: on the same
 // sweep the model's 128-row picks are within 0.6% of the per-shape best (8367
 // against 8322 us); 256-row tiles were ahead on down_proj of 70B alone, by 1-3%.
+//   * 128-row tiles in K halves (k_halves = 2: one 8-wave workgroup per CU
+//     runs both halves of its slice and sums them through LDS): a CU advances
+//     two chunks per 1.8 us, whatever the number of tiles (the two halves
+//     share one barrier per chunk, about 10% slower than two independent
+//     4-wave workgroups, far faster than one alone); the LDS sum adds 0.5 us
+//     per round.  Fitted to graph periods of every (k_halves, slices) plan on
+//     the Llama-3-8B layers at M = 256..4096 and the 70B layers at M =
+//     256..2048 (29 shapes): the picks total 7844 us against 7841 for the
+//     per-shape best and 7892 without K halves.  They win where the tiles
+//     leave CUs alone or would need fp32 partials: 8B qkv M = 1024 56.6 us
+//     (69.0 unsplit or on 2 slices), o M = 2048 65.7 (73.2), gate_up M = 256
+//     63.1 (69.8), o M = 1024 on 2 slices 46.9 (50.0).
 struct Prefill256Plan {
     int rows;
     int64_t splits;
+    int k_halves = 1;
 };
 
 // Exact scaling of the 256-wide prefill kernel with fp16 activations (see
@@ -178,40 +198,48 @@ bool prefill_exact_enabled() {
 }
 
 // only128: 128-row tiles only (exact scaling); max_splits: the most K slices
-// the plan may use.
+// the plan may use; khalves: 0 the model's choice, 1 or 2 that many K halves
+// for 128-row tiles.
 Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, bool only128, int64_t max_splits,
-                               double* cost_us = nullptr) {
-    constexpr double kChunk256 = 1.6, kChunk128Solo = 1.1, kChunk128Pair = 1.6, kPartialBps = 6.0e12,
-                     kCombineUs = 1.0;
+                               double* cost_us = nullptr, int khalves = 0) {
+    constexpr double kChunk256 = 1.6, kChunk128Solo = 1.1, kChunk128Pair = 1.6, kChunkHalves = 1.8,
+                     kHalvesSum = 0.5, kPartialBps = 6.0e12, kCombineUs = 1.0;
     Prefill256Plan best{256, 1};
     double best_us = 0.0;
     bool have = false;
     const int64_t num_n = ceil_div(N, 256);
     for (int rows : {256, 128}) {
         if (only128 && rows != 128) continue;
-        for (int64_t s : {1, 2, 3, 4, 6, 8}) {
-            if (s > nchunks || s > max_splits) break;
-            const int64_t cps = ceil_div(nchunks, s);
-            const int64_t sl = ceil_div(nchunks, cps);
-            if (s > 1 && sl != s) continue;  // the same plan as a smaller s
-            double us;
-            if (rows == 256) {
-                double waves = (double)ceil_div(ceil_div(M, 256) * num_n * s, cus);
-                if (s == 1) prefill256_tail_cols(M, N, cus, &waves);
-                us = waves * (double)cps * kChunk256;
-            } else {
-                // rounds of two per CU, and a last round of at most one per CU
-                // at the solo rate
-                const int64_t wgs = ceil_div(M, 128) * num_n * s;
-                const int64_t pairs = wgs / (2 * (int64_t)cus), rest = wgs - pairs * 2 * (int64_t)cus;
-                us = (double)cps * ((double)pairs * kChunk128Pair +
-                                    (rest == 0 ? 0.0 : rest <= cus ? kChunk128Solo : kChunk128Pair));
-            }
-            if (s > 1) us += (double)s * (double)M * (double)N * 8.0 / kPartialBps * 1e6 + kCombineUs;
-            if (!have || us < best_us) {
-                best = {rows, s};
-                best_us = us;
-                have = true;
+        for (int kh : {1, 2}) {
+            if (kh == 2 && rows != 128) continue;
+            if (khalves != 0 && rows == 128 && kh != khalves) continue;
+            for (int64_t s : {1, 2, 3, 4, 6, 8}) {
+                if (s > nchunks || s > max_splits) break;
+                const int64_t cps = ceil_div(nchunks, s);
+                const int64_t sl = ceil_div(nchunks, cps);
+                if (s > 1 && sl != s) continue;  // the same plan as a smaller s
+                double us;
+                if (rows == 256) {
+                    double waves = (double)ceil_div(ceil_div(M, 256) * num_n * s, cus);
+                    if (s == 1) prefill256_tail_cols(M, N, cus, &waves);
+                    us = waves * (double)cps * kChunk256;
+                } else if (kh == 2) {
+                    const int64_t rounds = ceil_div(ceil_div(M, 128) * num_n * s, (int64_t)cus);
+                    us = (double)rounds * ((double)ceil_div(cps, 2) * kChunkHalves + kHalvesSum);
+                } else {
+                    // rounds of two per CU, and a last round of at most one per CU
+                    // at the solo rate
+                    const int64_t wgs = ceil_div(M, 128) * num_n * s;
+                    const int64_t pairs = wgs / (2 * (int64_t)cus), rest = wgs - pairs * 2 * (int64_t)cus;
+                    us = (double)cps * ((double)pairs * kChunk128Pair +
+                                        (rest == 0 ? 0.0 : rest <= cus ? kChunk128Solo : kChunk128Pair));
+                }
+                if (s > 1) us += (double)s * (double)M * (double)N * 8.0 / kPartialBps * 1e6 + kCombineUs;
+                if (!have || us < best_us) {
+                    best = {rows, s, kh};
+                    best_us = us;
+                    have = true;
+                }
             }
         }
     }
@@ -219,19 +247,22 @@ Prefill256Plan plan_prefill256(int64_t M, int64_t N, int64_t nchunks, int cus, b
     return best;
 }
 
-// Decode kernel or 128-row prefill tile at M = 28..32 (MARLIN layout).  There
+// Decode kernel or 128-row prefill tile at M = 29..32 (MARLIN layout).  There
 // the decode kernel runs two 16-row tiles per wave and K slices of the
-// activations, and streams a layer's weights at about 1.6 TB/s whatever its
-// shape; the prefill tile's time follows the plan model above, which reads
-// 1.2-1.45x low at these M (measured on MI355X, us, decode / prefill tile:
-// Llama-3-70B gate_up 8192 x 57344 at M = 28 140 / 131 and M = 32 145 / 133;
-// every other 8B and 70B layer faster on the decode kernel at M = 17..32, e.g.
-// 70B qkv M = 32 26.5 / 31.5, 70B down 69 / 78, 8B gate_up 36 / 44).  Below
-// M = 28 the decode kernel was faster on every layer (70B gate_up M = 24 113 /
-// 131).
+// activations, and streams a large layer's weights at about 1.6 TB/s; the
+// prefill tile's time follows the plan model above, which reads up to 1.25x
+// low at these M.  Measured on MI355X (graph periods, us, decode / prefill
+// tile, fp16 x): Llama-3-70B gate_up 8192 x 57344 M = 24 101 / 115, M = 28
+// 123 / 116, M = 32 128 / 118; 70B down 28672 x 8192 M = 24 52 / 62, M = 28
+// 55.5 / 61.6, M = 32 69.5 / 61.7 (K halves, 8 slices); every other 8B and 70B
+// layer faster on the decode kernel at M = 17..32 (70B qkv M = 32 27.0 / 30.0,
+// 8B gate_up 29.1 / 36.3, 8B down 25.0 / 32.0).  The prefill model is nearly
+// flat over M = 28..32 while the decode kernel slows down, so the crossing is
+// placed by M: from M = 29 on (at M = 28 that leaves 70B gate_up 7% slower on
+// the decode kernel and 70B down 11% faster).
 bool prefer_prefill_tile(int xt, int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
     constexpr double kDecodeBps = 1.6e12, kModelLow = 1.25;
-    if (M < 28 || !prefill256_ok(LAYOUT_MARLIN, xt, N, K, G)) return false;
+    if (M < 29 || !prefill256_ok(LAYOUT_MARLIN, xt, N, K, G)) return false;
     double prefill_us = 0.0;
     plan_prefill256(M, N, ceil_div(round_up(K, kMarlinBK), 64), cus, xt == X_F16 && prefill_exact_enabled(), 8,
                     &prefill_us);
@@ -248,6 +279,7 @@ struct Plan {
     int p_splits = 1;        // prefill K splits
     int p_cps = 0;           // prefill chunks per split
     int p_tile_rows = 256;   // 256-wide kernel: rows per tile
+    int p_k_halves = 1;      // 256-wide kernel, 128-row tiles: K halves per workgroup (1 or 2)
     bool use_partial = false;
     int splits = 1;
     size_t partial_bytes = 0;
@@ -511,10 +543,12 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         } else if (p.p256 && prefill_splits_override()) {
             s = std::min<int64_t>(prefill_splits_override(), std::max<int64_t>(nchunks, 1));
         } else if (p.p256) {
-            Prefill256Plan pp = plan_prefill256(M, N, nchunks, cus, p.p_exact, 8);
-            if (!fits(pp.splits)) pp = plan_prefill256(M, N, nchunks, cus, p.p_exact, 1);
+            const int kh = prefill_khalves_override();
+            Prefill256Plan pp = plan_prefill256(M, N, nchunks, cus, p.p_exact, 8, nullptr, kh);
+            if (!fits(pp.splits)) pp = plan_prefill256(M, N, nchunks, cus, p.p_exact, 1, nullptr, kh);
             s = pp.splits;
             p.p_tile_rows = pp.rows;
+            p.p_k_halves = pp.k_halves;
         } else if (base >= cus || nchunks < 8) {
             s = 1;
         } else {
@@ -531,6 +565,9 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         if (p.use_partial) p.partial_bytes = (size_t)p.splits * M * N * 4;
         if (p.p256 && prefill_rows_override()) p.p_tile_rows = prefill_rows_override();
         if (p.p_exact && !prefill_rows_override()) p.p_tile_rows = 128;
+        // forced and overridden slice counts take one K half unless overridden too
+        if (p.p256 && (forced || prefill_splits_override())) p.p_k_halves = std::max(prefill_khalves_override(), 1);
+        if (p.p_tile_rows != 128) p.p_k_halves = 1;
     }
     // act-order: x is gathered once per call into the workspace, for either
     // kernel (each decode workgroup would otherwise gather the same slice)
@@ -655,6 +692,7 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.n_end = (int)N;
         a.cus = cu_count();
         a.tile_rows = p.p_tile_rows;
+        a.k_halves = p.p_k_halves;
         a.exact = p.p_exact ? 1 : 0;
         a.y32 = silu || p.use_partial ? nullptr : ev.y32;
         e = p.p256 ? launch_prefill256(xt, stype, qzeros != nullptr, a, stream, ev)
@@ -798,8 +836,8 @@ int pw4_plan_describe(int layout, int x_dtype, int scale_dtype, int has_zp, int 
         n = std::snprintf(buf, len, "decode nb=%d wps=%d splits=%d tree=%d win=%d ring=%d mt=%d", p.dc.nb, p.dc.wps,
                           p.dc.splits, p.tree ? 1 : 0, p.dc.kwin > 0 ? 1 : 0, p.dc.ring, p.dc.mt);
     } else if (p.p256) {
-        n = std::snprintf(buf, len, "prefill256 rows=%d splits=%d exact=%d%s", p.p_tile_rows, p.p_splits,
-                          p.p_exact ? 1 : 0, p.repack_bytes ? " repack" : "");
+        n = std::snprintf(buf, len, "prefill256 rows=%d splits=%d exact=%d khalves=%d%s", p.p_tile_rows, p.p_splits,
+                          p.p_exact ? 1 : 0, p.p_k_halves, p.repack_bytes ? " repack" : "");
     } else {
         n = std::snprintf(buf, len, "prefill128 splits=%d", p.p_splits);
     }

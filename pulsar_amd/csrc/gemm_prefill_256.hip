@@ -119,12 +119,22 @@ __device__ __forceinline__ float exact_scale(float s) {
 // per lane, kept in VGPRs, and two waves per SIMD (256 registers each):
 // 128-row tiles (75-78 KB of LDS) run two workgroups per CU, 256-row tiles
 // (123-132 KB) one.
-template <bool BF16, typename ST, bool ZP, bool PARTIAL, int RT, bool EXACT>
-__global__ __launch_bounds__(64 * RT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+//
+// KS = 2 (128-row tiles only): eight waves in two K halves of four.  Half h
+// runs the 128-row tile's pipeline over the second half of the workgroup's
+// chunks (h = 1) or the first (h = 0) in LDS stages of its own, both halves
+// meeting at the same barriers; at the end half 1 hands its accumulators to
+// half 0 through LDS, which adds them (first half + second half, the sum of
+// two K slices in slice order) and stores.  One such workgroup per CU (150-156
+// KB of LDS) runs a tile at the rate of two 128-row workgroups per CU with no
+// fp32 partials in memory.
+template <bool BF16, typename ST, bool ZP, bool PARTIAL, int RT, bool EXACT, int KS>
+__global__ __launch_bounds__(64 * RT * KS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
     static_assert(RT == 4 || RT == 8, "128- or 256-row tiles");
+    static_assert(KS == 1 || (KS == 2 && RT == 4), "K halves: 128-row tiles");
     static_assert(!EXACT || !BF16, "exact scaling: fp16 activations");
-    constexpr int NW = RT;                       // waves
+    constexpr int NW = RT;                       // waves of one K half
     constexpr int CT = 8 / RT;                   // 32-column MFMA tiles per wave
     constexpr int WPB = NW / 4;                  // waves per 64-column block
     constexpr int TMR = 32 * RT;                 // rows of this tile
@@ -132,15 +142,24 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
     constexpr int kARows = TMR / NW;             // activation rows each wave copies
     constexpr int kACopies = kARows / 8;         // one copy instruction moves 8 rows of 128 bytes
     constexpr int kBCopies = 2 / WPB;            // the block's two 1 KB weight tiles, shared by its waves
-    __shared__ __attribute__((aligned(16))) uint8_t sA[kStages][kAStage];
-    __shared__ __attribute__((aligned(16))) uint8_t sB[kStages][kBStage];
-    __shared__ __attribute__((aligned(16))) uint8_t sS[kStages][NW * kSlot];
-    __shared__ __attribute__((aligned(16))) uint8_t sZ[kStages][ZP ? NW * kSlot : 16];
+    constexpr int kZSlot = ZP ? NW * kSlot : 16;
+    // per K half: [stages] activations, then weights, scales, zero points
+    constexpr int kOffB = kStages * kAStage, kOffS = kOffB + kStages * kBStage, kOffZ = kOffS + kStages * NW * kSlot;
+    constexpr int kHalfBytes = kOffZ + kStages * kZSlot;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[KS * kHalfBytes];
+    static_assert(KS == 1 || NW * RT * CT * 16 * 64 * 4 <= KS * kHalfBytes, "the K-half sum fits the stages");
     // copies per wave per chunk: activations, weights, 1 scale, 1 zero point
     constexpr int kCopies = kACopies + kBCopies + 1 + (ZP ? 1 : 0);
 
     const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ks = KS == 2 ? wave_all / NW : 0;  // K half
+    const int wave = KS == 2 ? wave_all % NW : wave_all;
+    uint8_t* const half = smem + ks * kHalfBytes;
+    auto sA = [&](int st) { return half + st * kAStage; };
+    auto sB = [&](int st) { return half + kOffB + st * kBStage; };
+    auto sS = [&](int st) { return half + kOffS + st * NW * kSlot; };
+    auto sZ = [&](int st) { return half + kOffZ + st * kZSlot; };
     const int lane = tid & 63;
     const int c = lane & 31, hb = lane >> 5;
     const int cbl = wave / WPB, cth = wave % WPB;  // column block of the tile, 32-column half (8 waves)
@@ -161,9 +180,13 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
     const int n0 = a.n_begin + (in_group / gsz) * TN;
 
     const int split = blockIdx.z;
-    const int c_begin = split * a.chunks_per_split;
-    const int c_end = min(c_begin + a.chunks_per_split, a.nchunks);
-    const int nck = max(c_end - c_begin, 0);
+    const int c_first = split * a.chunks_per_split;
+    const int nck_all = max(min(c_first + a.chunks_per_split, a.nchunks) - c_first, 0);
+    // K halves: the first ceil(n / 2) chunks of the slice, then the rest;
+    // every wave runs niter barriers
+    const int niter = KS == 2 ? (nck_all + 1) / 2 : nck_all;
+    const int c_begin = c_first + ks * niter;
+    const int nck = ks ? nck_all - niter : niter;  // this wave's chunks
 
     const int ncb = (N + 63) / 64;              // MARLIN column blocks present
     const int cbw = min(n0 / 64 + cbl, ncb - 1);  // this wave's block (clamped: junk columns are never stored)
@@ -187,18 +210,18 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
     const uint32_t z_off = (uint32_t)min(ncol0 / 8 + lane, nw - 1) * 4u;
     const uint16_t* x_tile = a.x + (int64_t)m0 * K;
     auto issue = [&](int kc, int st, int g) {
-        const uint32_t abase = lds_addr(&sA[st][0]) + wave * kARows * 128;
+        const uint32_t abase = lds_addr(sA(st)) + wave * kARows * 128;
 #pragma unroll
         for (int i = 0; i < kACopies; ++i) lds_copy16(x_tile + kc * TK, a_off[i], abase + i * 1024);
         const uint32_t* wsrc = a.w + ((int64_t)cbw * a.nchunks + kc) * kChunkWords;
-        const uint32_t bbase = lds_addr(&sB[st][0]) + cbl * 2048;
+        const uint32_t bbase = lds_addr(sB(st)) + cbl * 2048;
 #pragma unroll
         for (int i = 0; i < kBCopies; ++i) {
             const int tt = cth * kBCopies + i;
             lds_copy16(wsrc, (uint32_t)(tt * 64 + lane) * 16u, bbase + tt * 1024);
         }
-        lds_copy4(scales + (int64_t)g * N, s_off, lds_addr(&sS[st][0]) + wave * kSlot);
-        if constexpr (ZP) lds_copy4(a.qzeros + (int64_t)g * nw, z_off, lds_addr(&sZ[st][0]) + wave * kSlot);
+        lds_copy4(scales + (int64_t)g * N, s_off, lds_addr(sS(st)) + wave * kSlot);
+        if constexpr (ZP) lds_copy4(a.qzeros + (int64_t)g * nw, z_off, lds_addr(sZ(st)) + wave * kSlot);
     };
 
     f32x16 acc[RT][CT];
@@ -238,8 +261,8 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
     // A fragments, the dequantized B) are fetched while step s's MFMAs run.
     // new_group (exact mode): this chunk starts a quant group after another one.
     auto compute = [&](int st, bool new_group) {
-        const uint8_t* A = &sA[st][0];
-        const uint8_t* B = &sB[st][0] + cbl * 2048;
+        const uint8_t* A = sA(st);
+        const uint8_t* B = sB(st) + cbl * 2048;
         u32x4 wq[2][CT];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -254,12 +277,12 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
             const int cl = (cth * CT + ct) * 32 + c;  // column inside the block
             float sf;
             if constexpr (sizeof(ST) == 4) {
-                sf = *reinterpret_cast<const float*>(&sS[st][wave * kSlot + cl * 4]);
+                sf = *reinterpret_cast<const float*>(sS(st) + wave * kSlot + cl * 4);
             } else {
-                sf = (float)*reinterpret_cast<const _Float16*>(&sS[st][wave * kSlot + cl * 2]);
+                sf = (float)*reinterpret_cast<const _Float16*>(sS(st) + wave * kSlot + cl * 2);
             }
             uint32_t z = 8u;
-            if constexpr (ZP) z = (*reinterpret_cast<const uint32_t*>(&sZ[st][wave * kSlot + (cl >> 3) * 4]) >> (4 * (cl & 7))) & 0xfu;
+            if constexpr (ZP) z = (*reinterpret_cast<const uint32_t*>(sZ(st) + wave * kSlot + (cl >> 3) * 4) >> (4 * (cl & 7))) & 0xfu;
             if constexpr (BF16) {
                 sb[ct] = (float)(__bf16)sf;
                 cz[ct] = -(128.f + (float)z) * sb[ct];
@@ -342,7 +365,7 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
     if (nck > 1) issue(c_begin + 1, 1, next_group());
     int gk = EXACT ? c_begin % cpg : 0;  // place of the chunk being computed in its group
     int st = 0, st2 = 2;                 // stages of chunks i and i + 2
-    for (int i = 0; i < nck; ++i) {
+    for (int i = 0; i < niter; ++i) {
         if (i + 1 < nck) {
             wait_vmcnt<kCopies>();  // this wave's copies of chunk i have landed
         } else {
@@ -350,7 +373,9 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
         }
         __syncthreads();            // everyone's have; everyone is done with chunk i - 1
         if (i + 2 < nck) issue(c_begin + i + 2, st2, next_group());
-        compute(st, i > 0 && gk == 0);
+        // (KS = 2: the second half may have one chunk fewer; it still joins
+        // the barrier of the last iteration)
+        if (KS == 1 || i < nck) compute(st, i > 0 && gk == 0);
         if constexpr (EXACT) gk = gk + 1 == cpg ? 0 : gk + 1;
         st = st == kStages - 1 ? 0 : st + 1;
         st2 = st2 == kStages - 1 ? 0 : st2 + 1;
@@ -362,6 +387,37 @@ void prefill256_kernel(const PrefillArgs a, const NibbleMasks mk) {
             for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[rt][ct][e] *= s_run[ct];
+    }
+    if constexpr (KS == 2) {
+        // the second half's accumulators to the first through LDS (the stages
+        // are free once every wave is past its last chunk): 16-byte rows,
+        // lane-consecutive, [wave][tile][e / 4][lane]
+        f32x4* red = reinterpret_cast<f32x4*>(smem);
+        __syncthreads();
+        if (ks == 1) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                    for (int e4 = 0; e4 < 4; ++e4) {
+                        const f32x4 v{acc[rt][ct][4 * e4], acc[rt][ct][4 * e4 + 1], acc[rt][ct][4 * e4 + 2],
+                                      acc[rt][ct][4 * e4 + 3]};
+                        red[(((wave * RT + rt) * CT + ct) * 4 + e4) * 64 + lane] = v;
+                    }
+        }
+        __syncthreads();
+        if (ks == 1) return;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                for (int e4 = 0; e4 < 4; ++e4) {
+                    const f32x4 v = red[(((wave * RT + rt) * CT + ct) * 4 + e4) * 64 + lane];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[rt][ct][4 * e4 + j] += v[j];
+                }
     }
 
     // ---- epilogue: D lane holds column c, rows 8*(e/4) + 4*hb + e%4 ---------
@@ -510,27 +566,40 @@ void launch_variant(const PrefillArgs& a, hipStream_t stream, KernelEvents ev) {
     w.n_begin = 0;
     w.n_end = a.N;
     const bool exact = !BF16 && a.exact;
-    auto launch = [&](auto rt, dim3 grid, const PrefillArgs& args, hipEvent_t start, hipEvent_t stop, auto partial) {
+    auto launch = [&](auto rt, auto ksc, dim3 grid, const PrefillArgs& args, hipEvent_t start, hipEvent_t stop,
+                      auto partial) {
         constexpr int RT = decltype(rt)::value;
+        constexpr int KSV = decltype(ksc)::value;
         constexpr bool P = decltype(partial)::value;
+        const dim3 block(64 * RT * KSV);
         if constexpr (!BF16) {
             if (exact) {
-                launch_kernel(prefill256_kernel<false, ST, ZP, P, RT, true>, grid, dim3(64 * RT), 0, stream, start,
-                              stop, args, mk);
+                launch_kernel(prefill256_kernel<false, ST, ZP, P, RT, true, KSV>, grid, block, 0, stream, start, stop,
+                              args, mk);
                 return;
             }
         }
-        launch_kernel(prefill256_kernel<BF16, ST, ZP, P, RT, false>, grid, dim3(64 * RT), 0, stream, start, stop, args,
-                      mk);
+        launch_kernel(prefill256_kernel<BF16, ST, ZP, P, RT, false, KSV>, grid, block, 0, stream, start, stop, args, mk);
     };
-    auto full = [&](auto... v) { launch(std::integral_constant<int, 8>{}, v...); };
-    auto half = [&](auto... v) { launch(std::integral_constant<int, 4>{}, v...); };
+    using One = std::integral_constant<int, 1>;
+    using Two = std::integral_constant<int, 2>;
+    auto full = [&](auto... v) { launch(std::integral_constant<int, 8>{}, One{}, v...); };
+    auto half = [&](auto... v) { launch(std::integral_constant<int, 4>{}, One{}, v...); };
+    // 128-row tiles whose workgroup runs the chunks as two K halves (8 waves)
+    auto halves = [&](auto... v) { launch(std::integral_constant<int, 4>{}, Two{}, v...); };
+    const bool k2 = a.tile_rows == TM / 2 && a.k_halves == 2;
     if (a.partial != nullptr) {  // K slices: fp32 partials of 256- or 128-row tiles
-        if (a.tile_rows == TM / 2) {
+        if (k2) {
+            halves(dim3((unsigned)tiles128, 1, a.splits), w, ev.start, ev.stop, std::true_type{});
+        } else if (a.tile_rows == TM / 2) {
             half(dim3((unsigned)tiles128, 1, a.splits), w, ev.start, ev.stop, std::true_type{});
         } else {
             full(dim3((unsigned)(num_m * num_n), 1, a.splits), w, ev.start, ev.stop, std::true_type{});
         }
+        return;
+    }
+    if (k2) {  // one 8-wave workgroup per CU
+        halves(dim3((unsigned)tiles128), w, ev.start, ev.stop, std::false_type{});
         return;
     }
     if (a.tile_rows == TM / 2) {  // every tile 128 rows: twice the workgroups, two per CU

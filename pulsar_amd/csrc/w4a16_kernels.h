@@ -147,6 +147,8 @@ struct PrefillArgs {
     int n_begin, n_end;      // output columns a launch covers (set by the 256-tile launcher)
     int cus;                 // compute units of the device (tail balancing)
     int tile_rows;           // 256-wide kernel: 256-row tiles (tail balanced when unsplit) or 128-row tiles
+    int k_halves;            // 256-wide kernel, 128-row tiles: 2 runs each K slice as two halves in one
+                             // 8-wave workgroup summed through LDS, else 1
     int silu;                // 256-wide kernel, unsplit: y [M, N/2] = silu(gate) * up (see DecodeArgs)
     int exact;               // 256-wide kernel, fp16 x: B = u - z and the scale applied to the fp32
                              // accumulators per group

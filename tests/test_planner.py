@@ -1,14 +1,20 @@
 """The plans the library picks for the BASELINE layers, read through pw4_plan_describe
 (host logic only: nothing launches).  Each pinned choice is the measured-faster plan on
-MI355X (256 CUs; kernel or call times in the comments, us):
+MI355X (256 CUs; graph periods in the comments, us, fp16 x):
 
-* M = 28..32 on the decode kernel, except Llama-3-70B gate_up (8192 x 57344), which is
-  faster on the 128-row prefill tile (M = 28: 140 decode / 131 prefill; M = 32: 145 /
-  133); at M = 24 the decode kernel still wins there (113 / 131), and at M = 32 on every
-  other 8B and 70B layer (70B qkv 26.5 / 31.5, 70B down 69 / 78, 8B gate_up 36 / 44).
-* Prefill K slices: Llama-3-8B o unsplit at M = 2048 (74-82 against 80-84 on 2 slices),
-  2 slices at M = 1024 (51 against 52 on 4), gate_up unsplit at M = 256 (73-76 against
-  76-78 on 2), and the splits of the other layers as measured fastest.
+* M = 29..32 on the decode kernel, except Llama-3-70B gate_up (8192 x 57344: M = 32 128
+  decode / 118 prefill tile) and down (28672 x 8192: M = 32 69.5 / 61.7), which are faster
+  on the 128-row prefill tile; at M = 28 and below the decode kernel (70B down M = 28 55.5 /
+  61.6, 70B gate_up M = 24 101 / 115; M = 28 123 / 116 is the one measured miss), and at
+  M = 32 on every other 8B and 70B layer (70B qkv 27.0 / 30.0, 8B gate_up 29.1 / 36.3, 8B
+  down 25.0 / 32.0).
+* Prefill K slices and K halves (128-row tiles whose 8-wave workgroup sums two K halves in
+  LDS): Llama-3-8B qkv M = 1024 in K halves 56.6 (69.0 unsplit or on 2 slices), o M = 2048
+  in K halves 65.7 (73.2 unsplit), o M = 1024 on 2 slices in K halves 46.9 (50.0 without),
+  gate_up M = 256 in K halves 63.1 (69.8 unsplit), down M = 2048 in K halves 216.5 (224.3 on
+  2 slices), down M = 256 on 8 slices in K halves 42.4 (44.7 without), o M = 256 on 8
+  slices in K halves 24.7 (24.2 without: within 2%), and unsplit single-half tiles at
+  M = 4096 (qkv 183.6 against 193.2 in K halves, gate_up 815 against 878).
 """
 
 import ctypes
@@ -23,7 +29,8 @@ LAYOUT_CT, LAYOUT_MARLIN = 0, 1
 G = 128
 L8 = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 28672), "down": (14336, 4096)}
 L70 = {"qkv": (8192, 10240), "gate_up": (8192, 57344), "down": (28672, 8192)}
-OVERRIDES = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS", "PW4_PREFILL_EXACT", "PW4_PREFILL_TILE", "PW4_DECODE",
+OVERRIDES = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS", "PW4_PREFILL_KHALVES", "PW4_PREFILL_EXACT",
+             "PW4_PREFILL_TILE", "PW4_DECODE",
              "PW4_DECODE_NB", "PW4_DECODE_SPLITS", "PW4_DECODE_WPS", "PW4_DECODE_WIN")
 
 
@@ -41,22 +48,24 @@ def plan(lib, m, k, n, dtype=DTYPE_F16, layout=LAYOUT_MARLIN, zp=0, perm=0, silu
     return buf.value.decode()
 
 
-@pytest.mark.parametrize("m", [28, 32])
+@pytest.mark.parametrize("layer", ["gate_up", "down"])
+@pytest.mark.parametrize("m", [29, 32])
 @pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_BF16])
-def test_70b_gate_up_takes_the_prefill_tile_from_m28(lib, m, dtype):
-    k, n = L70["gate_up"]
+def test_70b_large_layers_take_the_prefill_tile_from_m29(lib, layer, m, dtype):
+    k, n = L70[layer]
     assert plan(lib, m, k, n, dtype).startswith("prefill256"), plan(lib, m, k, n, dtype)
     # act-order with zero points (config 4) plans the same way
     assert plan(lib, m, k, n, dtype, zp=1, perm=1).startswith("prefill256")
 
 
-@pytest.mark.parametrize("m", [1, 16, 17, 24])
-def test_70b_gate_up_decode_below_m28(lib, m):
-    k, n = L70["gate_up"]
+@pytest.mark.parametrize("layer", ["gate_up", "down"])
+@pytest.mark.parametrize("m", [1, 16, 17, 24, 28])
+def test_70b_large_layers_decode_to_m28(lib, layer, m):
+    k, n = L70[layer]
     assert plan(lib, m, k, n).startswith("decode"), plan(lib, m, k, n)
 
 
-@pytest.mark.parametrize("layer", ["8b_qkv", "8b_o", "8b_gate_up", "8b_down", "70b_qkv", "70b_down"])
+@pytest.mark.parametrize("layer", ["8b_qkv", "8b_o", "8b_gate_up", "8b_down", "70b_qkv"])
 @pytest.mark.parametrize("m", [1, 16, 28, 32])
 def test_other_layers_decode_up_to_m32(lib, layer, m):
     model, name = layer.split("_", 1)
@@ -77,17 +86,19 @@ def test_forced_splits_keep_the_decode_kernel(lib):
 
 
 @pytest.mark.parametrize("layer,m,want", [
-    ("o", 2048, "prefill256 rows=128 splits=1 exact=1"),
-    ("o", 1024, "prefill256 rows=128 splits=2 exact=1"),
-    ("o", 256, "prefill256 rows=128 splits=8 exact=1"),
-    ("gate_up", 256, "prefill256 rows=128 splits=1 exact=1"),
-    ("gate_up", 4096, "prefill256 rows=128 splits=1 exact=1"),
-    ("qkv", 1024, "prefill256 rows=128 splits=2 exact=1"),
-    ("qkv", 4096, "prefill256 rows=128 splits=1 exact=1"),
-    ("down", 256, "prefill256 rows=128 splits=8 exact=1"),
-    ("down", 1024, "prefill256 rows=128 splits=4 exact=1"),
-    ("down", 2048, "prefill256 rows=128 splits=2 exact=1"),
-    ("down", 4096, "prefill256 rows=128 splits=1 exact=1"),
+    ("o", 2048, "prefill256 rows=128 splits=1 exact=1 khalves=2"),
+    ("o", 1024, "prefill256 rows=128 splits=2 exact=1 khalves=2"),
+    ("o", 256, "prefill256 rows=128 splits=8 exact=1 khalves=2"),
+    ("gate_up", 256, "prefill256 rows=128 splits=1 exact=1 khalves=2"),
+    ("gate_up", 1024, "prefill256 rows=128 splits=1 exact=1 khalves=1"),
+    ("gate_up", 4096, "prefill256 rows=128 splits=1 exact=1 khalves=1"),
+    ("qkv", 1024, "prefill256 rows=128 splits=1 exact=1 khalves=2"),
+    ("qkv", 2048, "prefill256 rows=128 splits=1 exact=1 khalves=1"),
+    ("qkv", 4096, "prefill256 rows=128 splits=1 exact=1 khalves=1"),
+    ("down", 256, "prefill256 rows=128 splits=8 exact=1 khalves=2"),
+    ("down", 1024, "prefill256 rows=128 splits=4 exact=1 khalves=1"),
+    ("down", 2048, "prefill256 rows=128 splits=1 exact=1 khalves=2"),
+    ("down", 4096, "prefill256 rows=128 splits=1 exact=1 khalves=1"),
 ])
 def test_prefill_splits_8b(lib, layer, m, want):
     k, n = L8[layer]
@@ -95,8 +106,9 @@ def test_prefill_splits_8b(lib, layer, m, want):
 
 
 @pytest.mark.parametrize("layer,m,want", [
-    ("qkv", 256, "splits=6"), ("qkv", 1024, "splits=3"), ("qkv", 2048, "splits=2"), ("qkv", 4096, "splits=1"),
-    ("gate_up", 1024, "splits=1"), ("down", 256, "splits=8"), ("down", 1024, "splits=2"), ("down", 2048, "splits=1"),
+    ("qkv", 256, "splits=3 exact=1 khalves=2"), ("qkv", 1024, "splits=3"), ("qkv", 2048, "splits=2"),
+    ("qkv", 4096, "splits=1"), ("gate_up", 1024, "splits=1"), ("down", 256, "splits=8"), ("down", 1024, "splits=2"),
+    ("down", 2048, "splits=1"),
 ])
 def test_prefill_splits_70b(lib, layer, m, want):
     k, n = L70[layer]

@@ -66,7 +66,7 @@ def test_prefill_gptq(tile, sym, act, sdtype):
 
 @pytest.fixture
 def plan_env():
-    keys = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS", "PW4_PREFILL_EXACT")
+    keys = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS", "PW4_PREFILL_EXACT", "PW4_PREFILL_KHALVES")
     old = {k: os.environ.get(k) for k in keys}
     yield os.environ
     for k, v in old.items():
@@ -210,3 +210,61 @@ def test_prefill_split_sum_repeated_calls(plan_env, rows):
             first = y.clone()
         elif i == 3:
             assert torch.equal(y, first)
+
+
+@pytest.mark.parametrize("dtype,exact", [(torch.float16, "1"), (torch.float16, "0"), (torch.bfloat16, "0")],
+                         ids=["f16-exact", "f16-rounded", "bf16"])
+@pytest.mark.parametrize("splits", [1, 2, 3])
+@pytest.mark.parametrize("m,n,k,g", [(300, 520, 1024, 128), (129, 264, 1088, 64), (257, 200, 64, 64),
+                                     (65, 1032, 192, 64)])
+def test_prefill_k_halves_agree_with_oracle(plan_env, dtype, exact, splits, m, n, k, g):
+    """128-row tiles whose 8-wave workgroup runs each K slice as two halves and sums them
+    through LDS: against the oracle with K slices of an even, odd (17 chunks: the second
+    half is one chunk short) and single chunk (the second half is empty), fp16 and fp32
+    scales."""
+    plan_env["PW4_PREFILL_ROWS"] = "128"
+    plan_env["PW4_PREFILL_KHALVES"] = "2"
+    plan_env["PW4_PREFILL_SPLITS"] = str(splits)
+    plan_env["PW4_PREFILL_EXACT"] = exact
+    c = reference_case(m, n, k, g, dtype, seed=23)
+    wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float32), g)
+    what = f"k halves {dtype} exact={exact} splits={splits} m={m} n={n} k={k}"
+    check(ops.gemm_w4a16_marlin(c.x, wm, sm, g), c.y_ref, dtype, what + " fp32 scales")
+    check(ops.gemm_w4a16_gptq(c.x, wm, sm.half(), None, None, g), c.y_ref, dtype, what + " fp16 scales")
+
+
+@pytest.mark.parametrize("dtype,exact", [(torch.float16, "1"), (torch.float16, "0"), (torch.bfloat16, "0")],
+                         ids=["f16-exact", "f16-rounded", "bf16"])
+@pytest.mark.parametrize("k", [2048, 2112])
+def test_prefill_k_halves_equal_two_slices(plan_env, dtype, exact, k):
+    """Unsplit in two K halves is the two-slice plan summed in the kernel: the same slice
+    boundary (ceil(chunks / 2)), the same fp32 sum first slice + second, one rounding --
+    bit-identical to the two-slice plan's combine pass."""
+    m, n, g = 700, 1032, 64
+    c = reference_case(m, n, k, g, dtype, seed=24)
+    wm, sm = ops.repack_w4a16(c.ct_packed(), c.scale(torch.float32), g)
+    plan_env["PW4_PREFILL_ROWS"] = "128"
+    plan_env["PW4_PREFILL_EXACT"] = exact
+    ys = {}
+    for kh, s in ((2, 1), (1, 2)):
+        plan_env["PW4_PREFILL_KHALVES"] = str(kh)
+        plan_env["PW4_PREFILL_SPLITS"] = str(s)
+        ys[kh] = ops.gemm_w4a16_marlin(c.x, wm, sm, g)
+    check(ys[2], c.y_ref, dtype, f"k halves {dtype} exact={exact} k={k}")
+    assert torch.equal(ys[2], ys[1]), (ys[2].float() - ys[1].float()).abs().max().item()
+
+
+@pytest.mark.parametrize("splits", [1, 2])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_k_halves_gptq(plan_env, splits, dtype):
+    """K halves with zero points and act-order (config 4's operators)."""
+    plan_env["PW4_PREFILL_ROWS"] = "128"
+    plan_env["PW4_PREFILL_KHALVES"] = "2"
+    plan_env["PW4_PREFILL_SPLITS"] = str(splits)
+    m, n, k, g = 390, 328, 1024, 64
+    c = baseline_case(m, n, k, g, dtype=dtype, seed=25, symmetric=False, act_order=True)
+    g_idx = torch.from_numpy(c.g_idx).cuda()
+    wm, perm = ops.repack_w4a16_gptq(c.qweight(), g_idx, g)
+    scales = torch.from_numpy(np.ascontiguousarray(c.scale_nk.T)).half().cuda()
+    y = ops.gemm_w4a16_gptq(c.x, wm, scales, c.qzeros(), perm, g)
+    check(y, c.y_ref, dtype, f"k halves gptq act-order {dtype} splits={splits}")

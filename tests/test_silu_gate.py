@@ -80,7 +80,7 @@ def _silu_ref(y_full: np.ndarray) -> np.ndarray:
 
 @pytest.fixture
 def plan_env():
-    keys = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS", "PW4_PREFILL_TILE")
+    keys = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS", "PW4_PREFILL_TILE", "PW4_PREFILL_KHALVES")
     old = {k: os.environ.get(k) for k in keys}
     yield os.environ
     for k, v in old.items():
@@ -111,6 +111,11 @@ CASES = [
     (129, 512, 2048, torch.float16, {"PW4_PREFILL_SPLITS": "4"}, True),    # 256-wide, K slices -> combine
     (300, 1040, 1024, torch.bfloat16, {"PW4_PREFILL_SPLITS": "3", "PW4_PREFILL_ROWS": "256"}, False),  # 8 waves
     (129, 512, 2048, torch.float16, {"PW4_PREFILL_SPLITS": "12"}, True),   # 256-wide, 12 slices
+    # 128-row tiles in two K halves (8 waves): gated in the epilogue, or in the combine
+    (300, 1024, 512, torch.float16, {"PW4_PREFILL_SPLITS": "1", "PW4_PREFILL_KHALVES": "2"}, True),
+    (200, 1024, 640, torch.bfloat16, {"PW4_PREFILL_SPLITS": "1", "PW4_PREFILL_KHALVES": "2", "PW4_PREFILL_ROWS": "128"},
+     False),
+    (129, 512, 2048, torch.float16, {"PW4_PREFILL_SPLITS": "2", "PW4_PREFILL_KHALVES": "2"}, True),
     (100, 512, 4096, torch.bfloat16, {"PW4_PREFILL_TILE": "128"}, False),  # 128 x 128 kernel, K slices
     (700, 1024, 256, torch.float16, {"PW4_PREFILL_TILE": "128"}, False),   # 128 x 128 kernel, unsplit
 ]
