@@ -53,7 +53,9 @@ Also reported:
                   decode bytes (the kernel's own duration): frac_of_read_floor
                   is that time over the decode kernel's, per shape and mean;
   prefill_dense_fp16_yardstick = the dense fp16 library GEMM (hipBLASLt
-                  through torch) at the M = 4096 shapes;
+                  through torch) at every prefill shape; prefill_vs_dense is
+                  its time over the W4A16 call's, from events around each call
+                  ("call") and from back-to-back calls in one graph ("graph");
   repack        = repack_w4a16 per layer, GB/s of words and scales moved over
                   the kernels' own interval (and the whole call's time).
 
@@ -120,6 +122,33 @@ def _median_time(fn, reps: int) -> float:
         fn()
         ts.append(time.perf_counter() - t0)
     return sorted(ts)[len(ts) // 2]
+
+
+def graph_period_us(torch, fn, calls: int, replays: int = 3) -> float:
+    """Device time per call of `calls` back-to-back calls fn(0), fn(1), ... captured in one
+    HIP graph (no host work between them): the best of `replays` replays, in us."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(calls):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(replays):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        best = min(best, a.elapsed_time(b) * 1e3 / calls)
+    del graph
+    return best
 
 
 def cpu_baseline() -> dict:
@@ -757,8 +786,10 @@ def dense_yardstick(torch, dev, reps: int) -> dict:
             torch.cuda.synchronize()
             ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
             tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            gus = graph_period_us(torch, lambda i: torch.nn.functional.linear(x, ws[i % copies]), max(copies, 4))
             out[f"{name}_m{m}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
-                                   "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3)}
+                                   "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3), "graph_us": round(gus, 1),
+                                   "graph_TFLOP/s": round(2.0 * m * n * k / gus / 1e6, 1)}
             del x
         del ws
         torch.cuda.empty_cache()
@@ -988,8 +1019,11 @@ def main() -> int:
                 torch.cuda.synchronize()
                 ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
                 tf = 2.0 * pm * n * k / (ms * 1e-3) / 1e12
+                ws_ = weights[name]
+                gus = graph_period_us(torch, lambda i: gemm_fp16_scales(x, ws_[i % len(ws_)]), len(ws_))
                 out[f"{name}_m{pm}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
-                                        "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3)}
+                                        "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 3), "graph_us": round(gus, 1),
+                                        "graph_TFLOP/s": round(2.0 * pm * n * k / gus / 1e6, 1)}
                 del x
         return out
 
@@ -1074,6 +1108,12 @@ def main() -> int:
         "prefill": prefill,
         "prefill_bf16": prefill_bf16,
         "prefill_dense_fp16_yardstick": dense,
+        # dense time / W4A16 time per shape: above 1 the W4A16 GEMM is the faster; "call"
+        # from the events around each call (host time between them included), "graph"
+        # from back-to-back calls in one graph (device time only)
+        "prefill_vs_dense": None if not (prefill and dense) else {
+            key: {"call": round(dense[key]["us"] / v["us"], 3), "graph": round(dense[key]["graph_us"] / v["graph_us"], 3)}
+            for key, v in prefill.items() if key in dense},
         "repack": repack,
         "stack": stack,
         "act_order_70b": act_order,
