@@ -851,7 +851,9 @@ def main() -> int:
     ap.add_argument("--pmc-workload", choices=["decode", "prefill", "prefill-bf16"],
                     help="no timing: decode = the decode sweep's launches once each, then a 512 MiB copy (the "
                          "HBM counter calibration), for rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE; prefill = "
-                         "one M=4096 launch per layer, for MFMA counters (prefill-bf16: bf16 activations)")
+                         "one launch per layer at --pmc-m rows, for MFMA and traffic counters (prefill-bf16: "
+                         "bf16 activations), then the same 512 MiB copy")
+    ap.add_argument("--pmc-m", type=int, default=PREFILL_M[-1], help="rows of the prefill --pmc-workload")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode sweep (headline value null)")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise the two --pmc-workload counter CSVs into profiles/decode_traffic.json")
@@ -889,8 +891,10 @@ def main() -> int:
     if args.pmc_workload in ("prefill", "prefill-bf16"):
         xdt = torch.bfloat16 if args.pmc_workload == "prefill-bf16" else torch.float16
         for name, k, n in LLAMA8B:
-            x = torch.randn(PREFILL_M[-1], k, device=dev).to(xdt)
+            x = torch.randn(args.pmc_m, k, device=dev).to(xdt)
             gemm_fp16_scales(x, weights[name][0])
+        src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device=dev)
+        torch.empty_like(src).copy_(src)
         torch.cuda.synchronize()
         return 0
     if args.pmc_workload == "decode":
