@@ -135,6 +135,13 @@ int decode_splits_override() {
     const int v = std::atoi(e);
     return (v == 2 || v == 4 || v == 8) ? v : 0;
 }
+// Decode block scales forced on (1) or off (0) where they apply, for tests and
+// sweeps; -1 = by layer size.
+int decode_block_scales_override() {
+    const char* e = plan_env("PW4_DECODE_BLOCK_SCALES");
+    if (!e) return -1;
+    return e[0] == '0' ? 0 : e[0] == '1' ? 1 : -1;
+}
 
 // Windowed decode plans (one unit per workgroup, the activations staged in K
 // windows by copy waves) where the activation slice does not fit in LDS: by
@@ -463,12 +470,23 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         const int64_t kwn = 8 / (nb / 16);
         const int64_t spu = std::max<int64_t>(ceil_div(ceil_div(kps, 128), kwn), 1);
         dc.ring = spu <= 4 || dc.ngrp > 2 || M <= 8 ? 4 : 8;
+        // Block scales (one scale load per four steps, handed between lane
+        // groups) on layers of 24 MiB of weights or more.  Measured on MI355X,
+        // kernel only, medians of six interleaved runs over the 8B decode sweep
+        // (fp16 x, G = 128): gate_up 3.0-3.2% and down 0.8-2.6% faster at M = 1..16;
+        // o 3.8-6.1% and qkv 0-3.6% slower.  The small layers run at their
+        // read floor, where the exchange on a wave's first block (its only one
+        // on o) costs more than the three scale loads it saves.
+        const int bs_mode = decode_block_scales_override();
+        dc.block_scales = layout == LAYOUT_MARLIN && dc.ngrp == 1 && !win &&
+                          (bs_mode < 0 ? N * K / 2 >= (int64_t{24} << 20) : bs_mode == 1);
         // Persistent grid: one or two workgroups per CU (register and LDS
         // budget), then as few units per workgroup as possible with the
         // least per-CU load.
         int64_t per_cu_max =
             lds <= kDecodeLdsLimit
-                ? decode_blocks_per_cu(layout, bf ? X_BF16 : X_F16, stype, zp, dc.mt, dc.ngrp, dc.ring, tree, lds, win)
+                ? decode_blocks_per_cu(layout, bf ? X_BF16 : X_F16, stype, zp, dc.mt, dc.ngrp, dc.ring, tree, lds, win,
+                                       dc.block_scales)
                 : 0;
         if (per_cu_max <= 0) per_cu_max = std::max<int64_t>(std::min<int64_t>(2, (int64_t)(kLdsPerCu / std::max<size_t>(lds, 1))), 1);
         per_cu_max = std::min<int64_t>(per_cu_max, 2);
@@ -833,8 +851,9 @@ int pw4_plan_describe(int layout, int x_dtype, int scale_dtype, int has_zp, int 
                              group_size, has_perm != 0, num_splits, silu != 0);
     int n;
     if (p.decode) {
-        n = std::snprintf(buf, len, "decode nb=%d wps=%d splits=%d tree=%d win=%d ring=%d mt=%d", p.dc.nb, p.dc.wps,
-                          p.dc.splits, p.tree ? 1 : 0, p.dc.kwin > 0 ? 1 : 0, p.dc.ring, p.dc.mt);
+        n = std::snprintf(buf, len, "decode nb=%d wps=%d splits=%d tree=%d win=%d ring=%d mt=%d bs=%d", p.dc.nb,
+                          p.dc.wps, p.dc.splits, p.tree ? 1 : 0, p.dc.kwin > 0 ? 1 : 0, p.dc.ring, p.dc.mt,
+                          p.dc.block_scales ? 1 : 0);
     } else if (p.p256) {
         n = std::snprintf(buf, len, "prefill256 rows=%d splits=%d exact=%d khalves=%d%s", p.p_tile_rows, p.p_splits,
                           p.p_exact ? 1 : 0, p.p_k_halves, p.repack_bytes ? " repack" : "");

@@ -190,17 +190,24 @@ __host__ __device__ inline size_t red_floats(int mt) { return (size_t)2 * kWaves
 // compiler from moving LDS accesses across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <bool BF16, int LAYOUT, typename ST, int MT, int NGRP, bool ZP, int U, bool TREE, bool WIN>
+template <bool BF16, int LAYOUT, typename ST, int MT, int NGRP, bool ZP, int U, bool TREE, bool WIN, bool SBK>
 __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void decode_kernel(const DecodeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     __shared__ int s_last;
     constexpr int MP = MT * 16;
     static_assert(NGRP == 1 || NGRP == 2 || NGRP == 4 || NGRP == 8, "quant groups per 128-K step");
-    // vector memory instructions per ring step (weights, scales, zero points)
+    // Block scales (SBK; MARLIN, one quant group per step): the scale (and
+    // zero point) of the four steps of a ring block come in one load per lane
+    // at the block's first step -- lane group h fetches step h's -- and reach
+    // the other lane groups through ds_bpermute, in place of one load per step.
+    constexpr bool SB = SBK && LAYOUT == LAYOUT_MARLIN && NGRP == 1 && !WIN && U % 4 == 0;
+    // vector memory instructions per ring step (weights, scales, zero points);
+    // block scales: per four steps
     constexpr int kLoadsPerStep = 1 + NGRP + (ZP ? NGRP : 0);
+    constexpr int kLoadsPerRing = SB ? U + (U / 4) * (ZP ? 2 : 1) : U * kLoadsPerStep;
     // vmcnt is six bits: waiting for "all but the ring" waits for at most 63
     // younger loads (with more, a few ring loads are waited for as well)
-    constexpr int kRingLoads = U * kLoadsPerStep < 63 ? U * kLoadsPerStep : 63;
+    constexpr int kRingLoads = kLoadsPerRing < 63 ? kLoadsPerRing : 63;
 
     const int tid = threadIdx.x;
     // wave-uniform by construction; readfirstlane tells the compiler, so that
@@ -307,7 +314,10 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
     const int gshift = a.G_log2;  // G is a power of two on this path
     const int lane_w = (h >> 1) * kChunkWords + (h & 1) * 256 + (cw * 16 + c) * 4;
     const int lane_w_tail = (h & 1) * 256 + (cw * 16 + c) * 4;
-    auto load_step = [&](int u, int j, Step& o) {
+    // head: the first step of a ring block (a compile-time fact of the slot);
+    // with block scales only those load scales, for steps j + h.
+    auto load_step = [&](int u, int j, Step& o, bool head) {
+        const int jh = min(j + h, spu - 1);  // block scales: lane group h's step
         if (u >= n_units) {
             u = max(n_units - 1, 0);
             j = spu - 1;
@@ -331,6 +341,16 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
                 for (int q = 0; q < 4; ++q) o.w[q] = (t * 32 + q * 8 < K) ? a.w[off + q] : 0u;
             }
         }
+        if constexpr (SB) {
+            if (head) {
+                // past the workgroup's last unit (u clamped) the values are unused
+                const int sth = min(kw + jh * kwn, max(nsteps - 1, 0));
+                const int g = min((kb + sth * 128) >> gshift, a.Kg - 1);
+                o.s[0] = (scales + (int64_t)g * N)[ncol_c];
+                if constexpr (ZP) o.z[0] = (a.qzeros + (int64_t)g * (N >> 3))[ncol_c >> 3];
+            }
+            return;
+        }
         const int g0 = k0 >> gshift;
 #pragma unroll
         for (int gi = 0; gi < NGRP; ++gi) {
@@ -343,6 +363,21 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
             }
         }
     };
+    // Block scales at a block's first step: step t's scale and zero-point word
+    // for this lane's column, from lane (c, t) of the head slot's loads.
+    float sblk[4] = {1.f, 1.f, 1.f, 1.f};
+    uint32_t zblk[4] = {0u, 0u, 0u, 0u};
+    auto block_scales = [&](const Step& in) {
+        if constexpr (SB) {
+            const int sv = __builtin_bit_cast(int, load_scale(&in.s[0]));
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int src = (c + 16 * t) << 2;
+                sblk[t] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, sv));
+                if constexpr (ZP) zblk[t] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)in.z[0]);
+            }
+        }
+    };
 
     // Issue the ring in the refills' order (weights, scale per step): the
     // loop body's vmcnt waits must hold for its first block too, and loads
@@ -350,7 +385,7 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
     Step ring[U];
 #pragma unroll
     for (int i = 0; i < U; ++i) {
-        load_step(0, i, ring[i]);
+        load_step(0, i, ring[i], i % 4 == 0);
         __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -385,7 +420,8 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
     // this lane group's quant group in MFMAs 0-1 and in MFMAs 2-3 of a step
     const int g_lo = step_group<NGRP>(h, 0), g_hi = step_group<NGRP>(h, 2);
 
-    auto compute_step = [&](int u, int j, const Step& in) {
+    // t: the step's place in its ring block (block scales: sblk[t], zblk[t])
+    auto compute_step = [&](int u, int j, const Step& in, int t) {
         const int st = kw + j * kwn;
         if (j >= spu || st >= nsteps) return;  // padding, or an uneven K-wave split
         int kl = st * 128;
@@ -398,7 +434,10 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
         const int ncol_c = min(col0 + cw * 16 + c, N - 1);
         uint32_t zl[NGRP];
 #pragma unroll
-        for (int gi = 0; gi < NGRP; ++gi) zl[gi] = ZP ? (in.z[gi] >> (4 * (ncol_c & 7))) & 0xfu : 8u;
+        for (int gi = 0; gi < NGRP; ++gi) {
+            const uint32_t zw = SB ? zblk[t] : in.z[gi];
+            zl[gi] = ZP ? (zw >> (4 * (ncol_c & 7))) & 0xfu : 8u;
+        }
         f32x4 tmp[NGRP][MT];
 #pragma unroll
         for (int gi = 0; gi < NGRP; ++gi)
@@ -467,7 +506,7 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[mt][r] += load_scale(&in.s[gi]) * tmp[gi][mt][r];
+                for (int r = 0; r < 4; ++r) acc[mt][r] += (SB ? sblk[t] : load_scale(&in.s[gi])) * tmp[gi][mt][r];
     };
 
     // ---- K slices through a pairwise exchange tree ---------------------------
@@ -672,8 +711,9 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
 #pragma unroll
             for (int i = 0; i < U; ++i) {
                 win_sync(jb + i);
-                compute_step(u, jb + i, ring[i]);
-                load_step(tu, tj + i, ring[i]);
+                if (i % 4 == 0) block_scales(ring[i]);  // before the refill overwrites the head slot
+                compute_step(u, jb + i, ring[i], i % 4);
+                load_step(tu, tj + i, ring[i], i % 4 == 0);
                 // keep the refill right behind its step: without the barrier
                 // the scheduler batches all U computes first and drains the ring
                 __builtin_amdgcn_sched_barrier(0);
@@ -683,7 +723,8 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
 #pragma unroll
             for (int i = 0; i < U; ++i) {
                 win_sync((nblk - 1) * U + i);
-                compute_step(u, (nblk - 1) * U + i, ring[i]);
+                if (i % 4 == 0) block_scales(ring[i]);
+                compute_step(u, (nblk - 1) * U + i, ring[i], i % 4);
             }
         }
         finish_unit(u);
@@ -705,62 +746,67 @@ using DecodeFn = void (*)(const DecodeArgs);
 // variants (WIN) exist for the MARLIN layout and NGRP 1 and 2, without the
 // tree.
 template <bool BF16, int LAYOUT, typename ST, bool ZP, int U, int MT, bool TREE, bool WIN>
-DecodeFn pick_ngrp(int ngrp) {
+DecodeFn pick_ngrp(int ngrp, bool sb) {
     switch (ngrp) {
-        case 1: return decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN>;
-        case 2: return decode_kernel<BF16, LAYOUT, ST, MT, 2, ZP, U, TREE, WIN>;
+        case 1:
+            if constexpr (LAYOUT == LAYOUT_MARLIN && !WIN) {
+                if (sb) return decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN, true>;
+            }
+            return decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN, false>;
+        case 2: return decode_kernel<BF16, LAYOUT, ST, MT, 2, ZP, U, TREE, WIN, false>;
         case 4:
-            if constexpr (!TREE && !WIN && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 4, ZP, U, TREE, WIN>;
+            if constexpr (!TREE && !WIN && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 4, ZP, U, TREE, WIN, false>;
             return nullptr;
         case 8:
-            if constexpr (!TREE && !WIN && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 8, ZP, U, TREE, WIN>;
+            if constexpr (!TREE && !WIN && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 8, ZP, U, TREE, WIN, false>;
             return nullptr;
         default: return nullptr;
     }
 }
 
 template <bool BF16, int LAYOUT, typename ST, bool ZP, int U>
-DecodeFn pick_mt_u(int mt, int ngrp, bool tree, bool win) {
+DecodeFn pick_mt_u(int mt, int ngrp, bool tree, bool win, bool sb) {
     if (tree) {
         if (win) return nullptr;
-        if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, true, false>(ngrp);
-        if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, true, false>(ngrp);
+        if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, true, false>(ngrp, sb);
+        if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, true, false>(ngrp, sb);
         return nullptr;
     }
     if (win) {
         if constexpr (LAYOUT == LAYOUT_MARLIN) {
-            if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false, true>(ngrp);
-            if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false, true>(ngrp);
+            if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false, true>(ngrp, sb);
+            if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false, true>(ngrp, sb);
         }
         return nullptr;
     }
-    if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false, false>(ngrp);
-    if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false, false>(ngrp);
+    if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false, false>(ngrp, sb);
+    if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false, false>(ngrp, sb);
     return nullptr;
 }
 
 template <bool BF16, int LAYOUT, typename ST, bool ZP>
-DecodeFn pick_mt(int mt, int ngrp, int ring, bool tree, bool win) {
-    return ring == 4 ? pick_mt_u<BF16, LAYOUT, ST, ZP, 4>(mt, ngrp, tree, win)
-                     : pick_mt_u<BF16, LAYOUT, ST, ZP, kRing>(mt, ngrp, tree, win);
+DecodeFn pick_mt(int mt, int ngrp, int ring, bool tree, bool win, bool sb) {
+    return ring == 4 ? pick_mt_u<BF16, LAYOUT, ST, ZP, 4>(mt, ngrp, tree, win, sb)
+                     : pick_mt_u<BF16, LAYOUT, ST, ZP, kRing>(mt, ngrp, tree, win, sb);
 }
 
 template <bool BF16>
-DecodeFn pick_layout(int layout, int stype, bool zp, int mt, int ngrp, int ring, bool tree, bool win) {
+DecodeFn pick_layout(int layout, int stype, bool zp, int mt, int ngrp, int ring, bool tree, bool win, bool sb) {
     if (layout == LAYOUT_CT) {
-        return (zp || stype != S_F32) ? nullptr : pick_mt<BF16, LAYOUT_CT, float, false>(mt, ngrp, ring, tree, win);
+        return (zp || stype != S_F32) ? nullptr : pick_mt<BF16, LAYOUT_CT, float, false>(mt, ngrp, ring, tree, win, sb);
     }
     if (stype == S_F32) {
-        return zp ? pick_mt<BF16, LAYOUT_MARLIN, float, true>(mt, ngrp, ring, tree, win)
-                  : pick_mt<BF16, LAYOUT_MARLIN, float, false>(mt, ngrp, ring, tree, win);
+        return zp ? pick_mt<BF16, LAYOUT_MARLIN, float, true>(mt, ngrp, ring, tree, win, sb)
+                  : pick_mt<BF16, LAYOUT_MARLIN, float, false>(mt, ngrp, ring, tree, win, sb);
     }
-    return zp ? pick_mt<BF16, LAYOUT_MARLIN, _Float16, true>(mt, ngrp, ring, tree, win)
-              : pick_mt<BF16, LAYOUT_MARLIN, _Float16, false>(mt, ngrp, ring, tree, win);
+    return zp ? pick_mt<BF16, LAYOUT_MARLIN, _Float16, true>(mt, ngrp, ring, tree, win, sb)
+              : pick_mt<BF16, LAYOUT_MARLIN, _Float16, false>(mt, ngrp, ring, tree, win, sb);
 }
 
-DecodeFn pick_decode(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree, bool win) {
-    return xtype == X_BF16 ? pick_layout<true>(layout, stype, zp, mt, ngrp, ring, tree, win)
-                           : pick_layout<false>(layout, stype, zp, mt, ngrp, ring, tree, win);
+DecodeFn pick_decode(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree, bool win,
+                     bool sb) {
+    return xtype == X_BF16 ? pick_layout<true>(layout, stype, zp, mt, ngrp, ring, tree, win, sb)
+                           : pick_layout<false>(layout, stype, zp, mt, ngrp, ring, tree, win, sb);
 }
 
 hipError_t prepare(DecodeFn fn, size_t lds) {
@@ -839,8 +885,8 @@ size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_s
 int decode_threads() { return kThreads; }
 
 int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree,
-                         size_t lds, bool windowed) {
-    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, mt, ngrp, ring, tree, windowed);
+                         size_t lds, bool windowed, bool block_scales) {
+    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, mt, ngrp, ring, tree, windowed, block_scales);
     if (fn == nullptr) return 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
@@ -867,7 +913,7 @@ int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          hipStream_t stream, KernelEvents ev) {
     const bool win = cfg.kwin > 0;
-    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp, cfg.ring, cfg.tree, win);
+    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp, cfg.ring, cfg.tree, win, cfg.block_scales);
     if (fn == nullptr) return hipErrorInvalidValue;
     // the kernel maps slots to rows with a multiply-high by spr_recip, exact
     // while slot * spr < 2^32

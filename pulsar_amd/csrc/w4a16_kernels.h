@@ -96,6 +96,9 @@ struct DecodeConfig {
     int splits;  // K slices
     int k_per_split;
     int ring;    // weight-load ring depth in steps: 4 or 8
+    // one scale (and zero-point) load per four ring steps, handed between lane
+    // groups with ds_bpermute (MARLIN, G >= 128, not windowed); else one per step
+    bool block_scales = false;
     bool red_single;
     bool tree;   // K slices through the exchange tree (splits a power of two, M <= 32)
     // K window of a windowed plan, 0 for none: one slice, one unit per
@@ -116,7 +119,7 @@ int decode_threads();
 // Resident decode workgroups per CU for the kernel variant and LDS size
 // (0 when the variant does not exist or the runtime cannot tell).
 int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree,
-                         size_t lds, bool windowed = false);
+                         size_t lds, bool windowed = false, bool block_scales = false);
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          hipStream_t stream, KernelEvents ev = {});
