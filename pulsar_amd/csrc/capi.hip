@@ -135,6 +135,12 @@ int decode_splits_override() {
     const int v = std::atoi(e);
     return (v == 2 || v == 4 || v == 8) ? v : 0;
 }
+// Act-order gathered in the decode kernel's LDS: 0 never (the gather
+// launch), else where it applies; for tests and sweeps.
+int decode_perm_lds_override() {
+    const char* e = plan_env("PW4_DECODE_PERM_LDS");
+    return e && e[0] == '0' ? 0 : 1;
+}
 // Decode block scales forced on (1) or off (0) where they apply, for tests and
 // sweeps; -1 = by layer size.
 int decode_block_scales_override() {
@@ -480,15 +486,30 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         const int bs_mode = decode_block_scales_override();
         dc.block_scales = layout == LAYOUT_MARLIN && dc.ngrp == 1 && !win &&
                           (bs_mode < 0 ? N * K / 2 >= (int64_t{24} << 20) : bs_mode == 1);
+        // Act-order gathered in LDS by the decode kernel (x as given staged
+        // whole beside the slice), in place of a separate gather launch: one
+        // slice over all of K, 16-row tiles, the 4-step ring, one quant group
+        // per step, and both copies of x in LDS.
+        size_t lds_run = lds;
+        if (has_perm && decode_perm_lds_override() != 0 && layout == LAYOUT_MARLIN && !forced && s == 1 && !tree &&
+            !win && dc.mt == 1 && dc.ring == 4 && dc.ngrp == 1 && K % 8 == 0 && decode_perm_cols(K) > 0) {
+            const size_t lpx = decode_lds_bytes((int)M, (int)kps, dc.ngrp, zp_any, bf, red_single, false, (int)K);
+            if (lpx <= kDecodeLdsLimit) {
+                dc.perm_cols = decode_perm_cols(K);
+                lds_run = lpx;
+            }
+        }
         // Persistent grid: one or two workgroups per CU (register and LDS
         // budget), then as few units per workgroup as possible with the
         // least per-CU load.
         int64_t per_cu_max =
-            lds <= kDecodeLdsLimit
-                ? decode_blocks_per_cu(layout, bf ? X_BF16 : X_F16, stype, zp, dc.mt, dc.ngrp, dc.ring, tree, lds, win,
-                                       dc.block_scales)
+            lds_run <= kDecodeLdsLimit
+                ? decode_blocks_per_cu(layout, bf ? X_BF16 : X_F16, stype, zp, dc.mt, dc.ngrp, dc.ring, tree, lds_run,
+                                       win, dc.block_scales, dc.perm_cols)
                 : 0;
-        if (per_cu_max <= 0) per_cu_max = std::max<int64_t>(std::min<int64_t>(2, (int64_t)(kLdsPerCu / std::max<size_t>(lds, 1))), 1);
+        if (per_cu_max <= 0) {
+            per_cu_max = std::max<int64_t>(std::min<int64_t>(2, (int64_t)(kLdsPerCu / std::max<size_t>(lds_run, 1))), 1);
+        }
         per_cu_max = std::min<int64_t>(per_cu_max, 2);
         int64_t best_wps = 1, best_cost = INT64_MAX;
         for (int64_t per_cu = 1; per_cu <= per_cu_max; ++per_cu) {
@@ -510,7 +531,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         dc.wps = (int)best_wps;
         dc.k_per_split = (int)kps;
         dc.splits = (int)s;
-        dc.lds_bytes = lds;
+        dc.lds_bytes = lds_run;
         dc.red_single = red_single;
         dc.tree = tree;
         dc.kwin = win ? (int)kwin : 0;
@@ -588,7 +609,9 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         if (p.p_tile_rows != 128) p.p_k_halves = 1;
     }
     // act-order: x is gathered once per call into the workspace, for either
-    // kernel (each decode workgroup would otherwise gather the same slice)
+    // kernel (each decode workgroup would otherwise gather the same slice),
+    // unless the decode kernel gathers it in LDS; the buffer is kept in the
+    // workspace either way, for a permutation that is not 16-byte aligned
     if (has_perm) p.xperm_bytes = (size_t)M * K * 2;
     // SiLU gating is fused into the decode kernel's direct store, the 256-wide
     // prefill kernel's unsplit epilogue and the split-K combine; the other
@@ -648,7 +671,15 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
     }
     const int64_t kext = layout == LAYOUT_MARLIN ? round_up(K, kMarlinBK) : round_up(K, 32);
     const uint16_t* xin = reinterpret_cast<const uint16_t*>(x);
-    if (perm) {
+    // act-order in the decode kernel's LDS reads the permutation as 16-byte
+    // vectors; another alignment takes the gather launch and the plain plan
+    DecodeConfig dc = p.dc;
+    if (p.decode && dc.perm_cols && (reinterpret_cast<uintptr_t>(perm) & 15) != 0) {
+        dc.perm_cols = 0;
+        dc.lds_bytes = decode_lds_bytes((int)M, dc.k_per_split, dc.ngrp, true, xt == X_BF16, dc.red_single);
+    }
+    const bool perm_in_lds = p.decode && dc.perm_cols > 0;
+    if (perm && !perm_in_lds) {
         e = launch_gather_x(xin, perm, xperm, (int)M, (int)K, stream, gather_staged_override());
         if (e != hipSuccess) return hip_fail(e);
         xin = xperm;
@@ -656,6 +687,7 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
     if (p.decode) {
         DecodeArgs a{};
         a.x = xin;
+        a.perm = perm_in_lds ? perm : nullptr;
         a.w = w;
         a.scales = scales;
         a.qzeros = qzeros;
@@ -686,7 +718,7 @@ int run_gemm(int layout, const void* x, int x_dtype, const uint32_t* w, const vo
         a.ncg = (int)ceil_div(ncols, p.dc.nb);
         a.ups = (int)ceil_div(a.ncg, p.dc.wps);
         a.spr_recip = (uint32_t)(((uint64_t{1} << 32) + (uint64_t)(a.kwin / 8 + 1) - 1) / (uint64_t)(a.kwin / 8 + 1));
-        e = launch_decode(layout, xt, stype, qzeros != nullptr, p.dc, a, stream, ev);
+        e = launch_decode(layout, xt, stype, qzeros != nullptr, dc, a, stream, ev);
         if (e != hipSuccess) return hip_fail(e);
     } else {
         PrefillArgs a{};
@@ -851,9 +883,9 @@ int pw4_plan_describe(int layout, int x_dtype, int scale_dtype, int has_zp, int 
                              group_size, has_perm != 0, num_splits, silu != 0);
     int n;
     if (p.decode) {
-        n = std::snprintf(buf, len, "decode nb=%d wps=%d splits=%d tree=%d win=%d ring=%d mt=%d bs=%d", p.dc.nb,
+        n = std::snprintf(buf, len, "decode nb=%d wps=%d splits=%d tree=%d win=%d ring=%d mt=%d bs=%d px=%d", p.dc.nb,
                           p.dc.wps, p.dc.splits, p.tree ? 1 : 0, p.dc.kwin > 0 ? 1 : 0, p.dc.ring, p.dc.mt,
-                          p.dc.block_scales ? 1 : 0);
+                          p.dc.block_scales ? 1 : 0, p.dc.perm_cols);
     } else if (p.p256) {
         n = std::snprintf(buf, len, "prefill256 rows=%d splits=%d exact=%d khalves=%d%s", p.p_tile_rows, p.p_splits,
                           p.p_exact ? 1 : 0, p.p_k_halves, p.repack_bytes ? " repack" : "");

@@ -180,8 +180,15 @@ __device__ __forceinline__ float half_to_f32(uint16_t v) {
 //   X     [M][rowstride] halves, rowstride = kps + 8, padded to whole 1 KB
 //         copy blocks: the workgroup's activation slice in natural K order
 //   RED   [2][8 waves][MT*16][16] fp32: per-unit cross-wave sums, double buffered
+//   XN    (act-order in LDS only) [M][K] halves: x as given, padded to 1 KB,
+//         from which X is gathered
 __host__ __device__ inline size_t x_slots(int M, int kps) { return ((size_t)M * (kps / 8 + 1) + 63) / 64 * 64; }
 __host__ __device__ inline size_t red_floats(int mt) { return (size_t)2 * kWaves * mt * 16 * 16; }
+__host__ __device__ inline size_t xn_slots(int M, int K) { return ((size_t)M * (K / 8) + 63) / 64 * 64; }
+// act-order in LDS: 16-byte x columns (8 K positions) of the permutation each
+// thread gathers, loaded ahead of the weight ring, K <= 8 * PXC * 512: 2 up to
+// K = 8192 (16 VGPRs, two workgroups per CU still fit), 8 up to K = 32768
+constexpr int kPermColsMax = 8;
 
 // s_waitcnt lgkmcnt(0); s_barrier: a workgroup barrier over LDS traffic only.
 // __syncthreads() is a workgroup release fence plus the barrier, and once
@@ -190,12 +197,17 @@ __host__ __device__ inline size_t red_floats(int mt) { return (size_t)2 * kWaves
 // compiler from moving LDS accesses across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <bool BF16, int LAYOUT, typename ST, int MT, int NGRP, bool ZP, int U, bool TREE, bool WIN, bool SBK>
+// PXC > 0: act-order in LDS (one slice, not windowed): the workgroup copies x
+// as given into XN and gathers its slice X[m][j] = XN[m][perm[j]] itself, in
+// place of a separate gather launch; each thread gathers PXC 16-byte columns.
+template <bool BF16, int LAYOUT, typename ST, int MT, int NGRP, bool ZP, int U, bool TREE, bool WIN, bool SBK, int PXC>
 __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void decode_kernel(const DecodeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     __shared__ int s_last;
     constexpr int MP = MT * 16;
     static_assert(NGRP == 1 || NGRP == 2 || NGRP == 4 || NGRP == 8, "quant groups per 128-K step");
+    constexpr bool PX = PXC > 0;
+    static_assert(!PX || (!TREE && !WIN && LAYOUT == LAYOUT_MARLIN), "act-order in LDS: one slice, MARLIN");
     // Block scales (SBK; MARLIN, one quant group per step): the scale (and
     // zero point) of the four steps of a ring block come in one load per lane
     // at the block's first step -- lane group h fetches step h's -- and reach
@@ -296,7 +308,28 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
             return;
         }
     }
-    copy_window(0, wave, kWaves, WIN ? min(kvalid, a.kwin) : kvalid);
+    // act-order in LDS: x as given into XN (M * K halves, contiguous in both),
+    // then each thread's permutation columns, all ahead of the weight ring, so
+    // the gather below overlaps the ring's first round trip
+    const uint32_t xn_off = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(nslots * 16) + (uint32_t)(a.red_single ? red_floats(MT) * 2 : red_floats(MT) * 4));
+    u32x4 pcol[PX ? PXC : 1][2];
+    if constexpr (PX) {
+        const int nxs = M * (K / 8);  // 16-byte slots of x
+        for (int b = wave; b * 64 < nxs; b += kWaves) {
+            const int f = b * 64 + lane;
+            if (f < nxs) lds_copy16(a.x + (int64_t)f * 8, smem_base + xn_off + b * 1024);
+        }
+        // columns past K / 8 re-read the last one (unused): constant count, no branch
+#pragma unroll
+        for (int i = 0; i < PXC; ++i) {
+            const int s8 = min(tid + i * kThreads, K / 8 - 1);
+            pcol[i][0] = *reinterpret_cast<const u32x4*>(a.perm + s8 * 8);
+            pcol[i][1] = *reinterpret_cast<const u32x4*>(a.perm + s8 * 8 + 4);
+        }
+    } else {
+        copy_window(0, wave, kWaves, WIN ? min(kvalid, a.kwin) : kvalid);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- weight / scale / zero loads of the wave's t-th step ----------------
@@ -394,6 +427,29 @@ __global__ __launch_bounds__(WIN ? kThreads + 64 * kCopyWaves : kThreads) void d
         wait_vmcnt<kRingLoads>();  // this wave's slice copies are done; its ring is still in flight
     } else {
         wait_vmcnt<0>();
+    }
+    if constexpr (PX) {
+        // every wave's XN copies have landed (each waited for its own above);
+        // slot (row, s8) of X gathers XN[row][perm[8 s8 .. 8 s8 + 7]]
+        lds_barrier();
+        const uint16_t* XN = smem + xn_off / 2;
+#pragma unroll
+        for (int i = 0; i < PXC; ++i) {
+            const int s8 = tid + i * kThreads;
+            if (s8 >= K / 8) continue;
+            for (int row = 0; row < M; ++row) {
+                const uint16_t* xr = XN + row * K;
+                u32x4 v;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const int e = 2 * w;  // elements e, e + 1: perm entries e / 4 words in
+                    const uint32_t lo = xr[pcol[i][e >> 2][e & 3]];
+                    const uint32_t hi = xr[pcol[i][(e + 1) >> 2][(e + 1) & 3]];
+                    v[w] = lo | (hi << 16);
+                }
+                *reinterpret_cast<u32x4*>(smem + (row * spr + s8) * 8) = v;
+            }
+        }
     }
     // zero the slots the steps read past the real activations (windowed plans
     // have none: their slice is whole windows of real activations)
@@ -745,68 +801,90 @@ using DecodeFn = void (*)(const DecodeArgs);
 // (NGRP 4 and 8) exist for the 4-step ring without the tree only.  Windowed
 // variants (WIN) exist for the MARLIN layout and NGRP 1 and 2, without the
 // tree.
+// Act-order in LDS (px: 0, or the columns per thread, 2 or 8) exists for the
+// plans that take it: MARLIN, 16-row tiles, the 4-step ring, one slice, one
+// quant group per step.
 template <bool BF16, int LAYOUT, typename ST, bool ZP, int U, int MT, bool TREE, bool WIN>
-DecodeFn pick_ngrp(int ngrp, bool sb) {
+DecodeFn pick_ngrp(int ngrp, bool sb, int px) {
+    constexpr bool kPx = LAYOUT == LAYOUT_MARLIN && MT == 1 && U == 4 && !TREE && !WIN;
     switch (ngrp) {
         case 1:
             if constexpr (LAYOUT == LAYOUT_MARLIN && !WIN) {
-                if (sb) return decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN, true>;
+                if constexpr (kPx) {
+                    if (px == 2) {
+                        return sb ? decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN, true, 2>
+                                  : decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN, false, 2>;
+                    }
+                    if (px == kPermColsMax) {
+                        return sb ? decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN, true, kPermColsMax>
+                                  : decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN, false, kPermColsMax>;
+                    }
+                }
+                if (px) return nullptr;
+                if (sb) return decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN, true, 0>;
             }
-            return decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN, false>;
-        case 2: return decode_kernel<BF16, LAYOUT, ST, MT, 2, ZP, U, TREE, WIN, false>;
+            if (px) return nullptr;
+            return decode_kernel<BF16, LAYOUT, ST, MT, 1, ZP, U, TREE, WIN, false, 0>;
+        case 2:
+            if (px) return nullptr;
+            return decode_kernel<BF16, LAYOUT, ST, MT, 2, ZP, U, TREE, WIN, false, 0>;
         case 4:
-            if constexpr (!TREE && !WIN && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 4, ZP, U, TREE, WIN, false>;
+            if (px) return nullptr;
+            if constexpr (!TREE && !WIN && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 4, ZP, U, TREE, WIN, false, 0>;
             return nullptr;
         case 8:
-            if constexpr (!TREE && !WIN && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 8, ZP, U, TREE, WIN, false>;
+            if (px) return nullptr;
+            if constexpr (!TREE && !WIN && U == 4) return decode_kernel<BF16, LAYOUT, ST, MT, 8, ZP, U, TREE, WIN, false, 0>;
             return nullptr;
         default: return nullptr;
     }
 }
 
 template <bool BF16, int LAYOUT, typename ST, bool ZP, int U>
-DecodeFn pick_mt_u(int mt, int ngrp, bool tree, bool win, bool sb) {
+DecodeFn pick_mt_u(int mt, int ngrp, bool tree, bool win, bool sb, int px) {
     if (tree) {
         if (win) return nullptr;
-        if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, true, false>(ngrp, sb);
-        if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, true, false>(ngrp, sb);
+        if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, true, false>(ngrp, sb, px);
+        if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, true, false>(ngrp, sb, px);
         return nullptr;
     }
     if (win) {
         if constexpr (LAYOUT == LAYOUT_MARLIN) {
-            if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false, true>(ngrp, sb);
-            if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false, true>(ngrp, sb);
+            if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false, true>(ngrp, sb, px);
+            if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false, true>(ngrp, sb, px);
         }
         return nullptr;
     }
-    if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false, false>(ngrp, sb);
-    if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false, false>(ngrp, sb);
+    if (mt == 1) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 1, false, false>(ngrp, sb, px);
+    if (mt == 2) return pick_ngrp<BF16, LAYOUT, ST, ZP, U, 2, false, false>(ngrp, sb, px);
     return nullptr;
 }
 
 template <bool BF16, int LAYOUT, typename ST, bool ZP>
-DecodeFn pick_mt(int mt, int ngrp, int ring, bool tree, bool win, bool sb) {
-    return ring == 4 ? pick_mt_u<BF16, LAYOUT, ST, ZP, 4>(mt, ngrp, tree, win, sb)
-                     : pick_mt_u<BF16, LAYOUT, ST, ZP, kRing>(mt, ngrp, tree, win, sb);
+DecodeFn pick_mt(int mt, int ngrp, int ring, bool tree, bool win, bool sb, int px) {
+    return ring == 4 ? pick_mt_u<BF16, LAYOUT, ST, ZP, 4>(mt, ngrp, tree, win, sb, px)
+                     : pick_mt_u<BF16, LAYOUT, ST, ZP, kRing>(mt, ngrp, tree, win, sb, px);
 }
 
 template <bool BF16>
-DecodeFn pick_layout(int layout, int stype, bool zp, int mt, int ngrp, int ring, bool tree, bool win, bool sb) {
+DecodeFn pick_layout(int layout, int stype, bool zp, int mt, int ngrp, int ring, bool tree, bool win, bool sb,
+                     int px) {
     if (layout == LAYOUT_CT) {
-        return (zp || stype != S_F32) ? nullptr : pick_mt<BF16, LAYOUT_CT, float, false>(mt, ngrp, ring, tree, win, sb);
+        return (zp || stype != S_F32) ? nullptr
+                                      : pick_mt<BF16, LAYOUT_CT, float, false>(mt, ngrp, ring, tree, win, sb, px);
     }
     if (stype == S_F32) {
-        return zp ? pick_mt<BF16, LAYOUT_MARLIN, float, true>(mt, ngrp, ring, tree, win, sb)
-                  : pick_mt<BF16, LAYOUT_MARLIN, float, false>(mt, ngrp, ring, tree, win, sb);
+        return zp ? pick_mt<BF16, LAYOUT_MARLIN, float, true>(mt, ngrp, ring, tree, win, sb, px)
+                  : pick_mt<BF16, LAYOUT_MARLIN, float, false>(mt, ngrp, ring, tree, win, sb, px);
     }
-    return zp ? pick_mt<BF16, LAYOUT_MARLIN, _Float16, true>(mt, ngrp, ring, tree, win, sb)
-              : pick_mt<BF16, LAYOUT_MARLIN, _Float16, false>(mt, ngrp, ring, tree, win, sb);
+    return zp ? pick_mt<BF16, LAYOUT_MARLIN, _Float16, true>(mt, ngrp, ring, tree, win, sb, px)
+              : pick_mt<BF16, LAYOUT_MARLIN, _Float16, false>(mt, ngrp, ring, tree, win, sb, px);
 }
 
 DecodeFn pick_decode(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree, bool win,
-                     bool sb) {
-    return xtype == X_BF16 ? pick_layout<true>(layout, stype, zp, mt, ngrp, ring, tree, win, sb)
-                           : pick_layout<false>(layout, stype, zp, mt, ngrp, ring, tree, win, sb);
+                     bool sb, int px) {
+    return xtype == X_BF16 ? pick_layout<true>(layout, stype, zp, mt, ngrp, ring, tree, win, sb, px)
+                           : pick_layout<false>(layout, stype, zp, mt, ngrp, ring, tree, win, sb, px);
 }
 
 hipError_t prepare(DecodeFn fn, size_t lds) {
@@ -876,17 +954,22 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
 
 }  // namespace
 
-size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single, bool windowed) {
+size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single, bool windowed, int k_perm) {
     const int mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     size_t b = x_slots(M, kps) * 16 * (windowed ? 2 : 1) + red_floats(mt) * 4 / (red_single ? 2 : 1);
+    if (k_perm > 0) b += xn_slots(M, k_perm) * 16;
     return b;
+}
+
+int decode_perm_cols(int64_t K) {
+    return K <= 8 * 2 * kThreads ? 2 : K <= 8 * kPermColsMax * kThreads ? kPermColsMax : 0;
 }
 
 int decode_threads() { return kThreads; }
 
 int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree,
-                         size_t lds, bool windowed, bool block_scales) {
-    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, mt, ngrp, ring, tree, windowed, block_scales);
+                         size_t lds, bool windowed, bool block_scales, int perm_cols) {
+    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, mt, ngrp, ring, tree, windowed, block_scales, perm_cols);
     if (fn == nullptr) return 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
@@ -913,7 +996,8 @@ int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          hipStream_t stream, KernelEvents ev) {
     const bool win = cfg.kwin > 0;
-    const DecodeFn fn = pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp, cfg.ring, cfg.tree, win, cfg.block_scales);
+    const DecodeFn fn =
+        pick_decode(layout, xtype, stype, zp, cfg.mt, cfg.ngrp, cfg.ring, cfg.tree, win, cfg.block_scales, cfg.perm_cols);
     if (fn == nullptr) return hipErrorInvalidValue;
     // the kernel maps slots to rows with a multiply-high by spr_recip, exact
     // while slot * spr < 2^32
@@ -934,6 +1018,18 @@ hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const Decode
             return hipErrorInvalidValue;
         }
     } else if (a.kwin != a.k_per_split) {
+        return hipErrorInvalidValue;
+    }
+    if (cfg.perm_cols) {
+        // what the in-LDS gather rests on: one slice over all of K, x and the
+        // permutation present, each thread's columns within the variant's, and
+        // the LDS size holding XN behind the slice and the reduction buffers
+        if (a.perm == nullptr || a.splits != 1 || a.k_per_split < a.K || a.K % 8 != 0 ||
+            (int64_t)a.K > 8 * (int64_t)cfg.perm_cols * kThreads || a.M > 16 ||
+            cfg.lds_bytes < decode_lds_bytes(a.M, a.kwin, cfg.ngrp, zp, xtype == X_BF16, cfg.red_single, false, a.K)) {
+            return hipErrorInvalidValue;
+        }
+    } else if (a.perm != nullptr) {
         return hipErrorInvalidValue;
     }
     hipError_t e = prepare(fn, cfg.lds_bytes);

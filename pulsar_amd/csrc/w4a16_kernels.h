@@ -53,7 +53,8 @@ struct NibbleMasks {
 };
 
 struct DecodeArgs {
-    const uint16_t* x;       // [M, K] fp16 / bf16 bits (already act-order permuted when needed)
+    const uint16_t* x;       // [M, K] fp16 / bf16 bits (already act-order permuted, unless perm is given)
+    const int32_t* perm;     // act-order in LDS (DecodeConfig::perm_cols): the K permutation, x as given; else null
     const uint32_t* w;       // MARLIN words, or CT [N, K/8]
     const void* scales;      // MARLIN: [Kg, N]; CT: [N, Kg] fp32
     const uint32_t* qzeros;  // [Kg, N/8] (MARLIN, asymmetric) or null
@@ -99,6 +100,9 @@ struct DecodeConfig {
     // one scale (and zero-point) load per four ring steps, handed between lane
     // groups with ds_bpermute (MARLIN, G >= 128, not windowed); else one per step
     bool block_scales = false;
+    // act-order gathered in LDS by the decode kernel itself (see DecodeArgs::perm):
+    // the permutation's 16-byte columns per thread (decode_perm_cols), 0 for none
+    int perm_cols = 0;
     bool red_single;
     bool tree;   // K slices through the exchange tree (splits a power of two, M <= 32)
     // K window of a windowed plan, 0 for none: one slice, one unit per
@@ -114,12 +118,17 @@ struct DecodeConfig {
 // red_single: one cross-wave reduction buffer instead of two (one more
 // barrier per unit), for plans whose activation slice leaves no room.
 // windowed: kps is the K window, staged in two buffers.
-size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single, bool windowed = false);
+// k_perm: K of x as given, staged whole for the in-LDS act-order gather, or 0.
+size_t decode_lds_bytes(int M, int kps, int ngrp, bool zp, bool bf16, bool red_single, bool windowed = false,
+                        int k_perm = 0);
+// Permutation columns per thread of the in-LDS act-order gather for K (2 or
+// 8), or 0 past what it takes.
+int decode_perm_cols(int64_t K);
 int decode_threads();
 // Resident decode workgroups per CU for the kernel variant and LDS size
 // (0 when the variant does not exist or the runtime cannot tell).
 int decode_blocks_per_cu(int layout, int xtype, int stype, bool zp, int mt, int ngrp, int ring, bool tree,
-                         size_t lds, bool windowed = false, bool block_scales = false);
+                         size_t lds, bool windowed = false, bool block_scales = false, int perm_cols = 0);
 
 hipError_t launch_decode(int layout, int xtype, int stype, bool zp, const DecodeConfig& cfg, const DecodeArgs& a,
                          hipStream_t stream, KernelEvents ev = {});
