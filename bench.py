@@ -571,32 +571,39 @@ def act_order_bench(torch, dev, steps: int, warmup: int) -> dict:
         for m in ACT_ORDER_M:
             x = torch.randn(m, k, device=dev, generator=gen).half()
 
-            def call(i):
+            def call(i, act=True):
                 w = ws[i % copies]
-                return pulsar_amd.ops.gemm_w4a16_gptq(x, w[0], w[1], w[2], w[3], G)
+                return pulsar_amd.ops.gemm_w4a16_gptq(x, w[0], w[1], w[2], w[3] if act else None, G)
 
             if m <= 16:
-                with torch.cuda.stream(stream):
-                    for i in range(copies):
-                        call(i)
-                stream.synchronize()
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph, stream=stream):
-                    outs = [call(i) for i in range(copies)]
-                for _ in range(warmup):
-                    graph.replay()
-                torch.cuda.synchronize()
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                with torch.cuda.stream(stream):
-                    a.record(stream)
-                    for _ in range(steps):
+                def period(act):
+                    with torch.cuda.stream(stream):
+                        for i in range(copies):
+                            call(i, act)
+                    stream.synchronize()
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph, stream=stream):
+                        outs = [call(i, act) for i in range(copies)]
+                    for _ in range(warmup):
                         graph.replay()
-                    b.record(stream)
-                torch.cuda.synchronize()
-                us = a.elapsed_time(b) * 1e3 / (steps * copies)
+                    torch.cuda.synchronize()
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    with torch.cuda.stream(stream):
+                        a.record(stream)
+                        for _ in range(steps):
+                            graph.replay()
+                        b.record(stream)
+                    torch.cuda.synchronize()
+                    del graph, outs
+                    return a.elapsed_time(b) * 1e3 / (steps * copies)
+
+                us = period(True)
+                # the same weights, scales and zero points without the permutation: the
+                # natural-order asymmetric call, so the ratio is what act-order costs
+                nat = period(False)
                 gbs = act_order_bytes(m, k, n) / (us * 1e-6) / 1e9
-                res[f"m{m}"] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
-                del graph, outs
+                res[f"m{m}"] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3),
+                                "natural_order_us": round(nat, 2), "over_natural_order": round(us / nat, 3)}
             else:
                 for i in range(2):
                     call(i)
