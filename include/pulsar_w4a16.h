@@ -89,7 +89,10 @@ int pw4_observe_next_call(float* y32);
 /* Diagnostic, no counterpart in the reference (it is for tests and tuning):
  * writes into buf (len bytes, NUL-terminated) the plan a GEMM call with these
  * arguments would run, e.g. "decode nb=16 wps=256 splits=1 tree=0 win=0 ring=4
- * mt=1" or "prefill256 rows=128 splits=2 exact=1".  layout: PW4_LAYOUT_CT
+ * mt=1 bs=1 px=0" (bs: one scale load per four steps; px: act-order gathered
+ * in the kernel's LDS, its permutation columns per thread) or "prefill256
+ * rows=128 splits=2 exact=1 khalves=2" (khalves: two K halves per 8-wave
+ * workgroup, summed in LDS).  layout: PW4_LAYOUT_CT
  * (pw4_gemm_w4a16) or PW4_LAYOUT_MARLIN (pw4_gemm_w4a16_marlin; with silu
  * nonzero pw4_gemm_w4a16_silu_mul).  Launches nothing.  The plan depends on
  * the current device's compute-unit count (256 assumed when no device
