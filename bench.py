@@ -57,7 +57,10 @@ Also reported:
                   its time over the W4A16 call's, from events around each call
                   ("call") and from back-to-back calls in one graph ("graph");
   repack        = repack_w4a16 per layer, GB/s of words and scales moved over
-                  the kernels' own interval (and the whole call's time).
+                  the kernels' own interval (and the whole call's time);
+  gptq_repack   = repack_w4a16_gptq of the Llama-3-8B and -70B layers, in natural
+                  order and through an act-order permutation: the repack
+                  kernel's own interval and GB/s of words read and written.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-prefill] [--no-cpu]
 """
@@ -769,6 +772,47 @@ def repack_bench(torch, dev) -> dict:
     return out
 
 
+def gptq_repack_bench(torch, dev) -> dict:
+    """repack_w4a16_gptq (GPTQ qweight [K/8, N] -> MARLIN) per Llama-3-8B and -70B linear
+    (q, k, gate, down; 70B qkv, gate_up, down), in natural order and with act-order g_idx
+    (a random permutation of the rows, G = 128).  us: the repack kernel's own interval
+    (pw4_time_next_kernel armed for the call; the permutation's own kernel, which runs first,
+    is not in it), median over 7 passes of rotating copies that hold >= 512 MB.  Bytes: the
+    qweight words read plus the MARLIN words written (2 * N * K / 2)."""
+    import pulsar_amd
+
+    lib = pulsar_amd.capi()
+    layers = [("8b_q", 4096, 4096), ("8b_k", 4096, 1024), ("8b_gate", 4096, 14336), ("8b_down", 14336, 4096)]
+    layers += [("70b_" + name, k, n) for name, k, n in LLAMA70B]
+    out = {}
+    for name, k, n in layers:
+        nbytes = n * k // 2 * 2
+        copies = max(2, min(16, -(-(512 << 20) // nbytes)))
+        qws = [torch.randint(-(2 ** 31), 2 ** 31, (k // 8, n), dtype=torch.int32, device=dev) for _ in range(copies)]
+        g_idx = torch.empty(k, dtype=torch.int32, device=dev)
+        g_idx[torch.randperm(k, device=dev)] = torch.arange(k, device=dev, dtype=torch.int32) // G
+        r = {"bytes": nbytes}
+        for label, gi in (("natural", None), ("act_order", g_idx)):
+            pulsar_amd.ops.repack_w4a16_gptq(qws[0], gi, G)
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(7 * copies)]
+            for a, b in ev:  # create the events before handing them over
+                a.record()
+                b.record()
+            for i, (a, b) in enumerate(ev):
+                if lib.pw4_time_next_kernel(a, b) != 0:
+                    raise RuntimeError("pw4_time_next_kernel failed")
+                pulsar_amd.ops.repack_w4a16_gptq(qws[i % copies], gi, G)
+            torch.cuda.synchronize()
+            us = sorted(a.elapsed_time(b) for a, b in ev)[len(ev) // 2] * 1e3
+            r[label] = {"us": round(us, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
+        out[name] = r
+        del qws, g_idx
+        torch.cuda.empty_cache()
+    return out
+
+
 def dense_yardstick(torch, dev, reps: int) -> dict:
     """What the dense fp16 library GEMM (torch.nn.functional.linear -> hipBLASLt) does at
     the prefill shapes (every M of the sweep) with the same kind of data (x ~ N(0,1),
@@ -1053,6 +1097,7 @@ def main() -> int:
         stack = stack_bench(torch, dev, args.steps, args.warmup)
 
     act_order = None if args.no_act_order else act_order_bench(torch, dev, args.steps, args.warmup)
+    gptq_repack = None if args.no_act_order else gptq_repack_bench(torch, dev)
 
     cpu = None if args.no_cpu else cpu_baseline()
     if cpu is not None:
@@ -1128,6 +1173,7 @@ def main() -> int:
         "repack": repack,
         "stack": stack,
         "act_order_70b": act_order,
+        "gptq_repack": gptq_repack,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

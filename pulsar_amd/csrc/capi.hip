@@ -74,6 +74,19 @@ const char* plan_env(const char* name) {
     return enabled ? std::getenv(name) : nullptr;
 }
 
+// Act-order repack overrides for tuning sweeps and tests: the column block
+// width (8, 16, 32 or 64) and the number of workgroups; unset = heuristic.
+int repack_cols_override() {
+    const char* e = plan_env("PW4_REPACK_COLS");
+    const int v = e ? std::atoi(e) : 0;
+    return (v == 8 || v == 16 || v == 32 || v == 64) ? v : 0;
+}
+int repack_grid_override() {
+    const char* e = plan_env("PW4_REPACK_GRID");
+    const int v = e ? std::atoi(e) : 0;
+    return v > 0 ? v : 0;
+}
+
 // Act-order gather override for tuning sweeps: 1 stages the rows in LDS, 0
 // reads them directly, -1 (unset) = heuristic.
 int gather_staged_override() {
@@ -1047,7 +1060,8 @@ int pw4_repack_gptq(const int32_t* qweight, const int32_t* perm, int64_t N, int6
     if (N > 0 && K > 0 && (!qweight || !weight_marlin)) return PW4_ERR_ARG;
     hipError_t e = launch_repack_gptq(reinterpret_cast<const uint32_t*>(qweight), perm,
                                       reinterpret_cast<uint32_t*>(weight_marlin), (int)N, (int)K,
-                                      reinterpret_cast<hipStream_t>(stream), ev.start, ev.stop, cu_count());
+                                      reinterpret_cast<hipStream_t>(stream), ev.start, ev.stop, cu_count(),
+                                      repack_cols_override(), repack_grid_override());
     if (e != hipSuccess) return hip_fail(e);
     return PW4_OK;
 }

@@ -143,126 +143,206 @@ __global__ __launch_bounds__(kRepackThreads) void repack_gptq_kernel(const uint3
     }
 }
 
-// GPTQ qweight [K/8, N] -> MARLIN through the act-order permutation: a
-// workgroup takes NB columns over the whole K.  It stages the columns' source
-// words (all K/8 rows) and the permutation (clamped to [0, K), 16 bits) in LDS,
-// then assembles the MARLIN words from nibbles gathered in LDS, so each source
-// word is read from HBM once (gathering straight from qweight reads it once per
-// nibble).  A thread takes 4 adjacent columns of one 32-K tile: each 8-entry run
-// of the permutation is one 16-byte LDS read shared by the tile's threads, and
-// each source row one 16-byte read for the 4 columns.  grid: Npad/NB.
-// Staging reads 4 adjacent columns of a row per 16-byte load (VEC: N % 4 == 0
-// and 16-byte aligned qweight; otherwise word by word), 8 loads in flight per
-// thread, and the permutation 4 entries per 16-byte load (K % 4 == 0 always:
-// K % 8 == 0 on this path).
+// 8 x 8 nibble transpose in registers: nibble j of a[i] moves to nibble i of
+// a[j].  Three rounds of block swaps -- 4-nibble halves and bytes with
+// v_perm_b32, single nibbles with masks -- 32 VALU instructions.
+__device__ __forceinline__ void transpose_nibbles8(uint32_t (&a)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = __builtin_amdgcn_perm(a[i + 4], a[i], 0x05040100u);  // halves 0 of a[i], a[i+4]
+        const uint32_t hi = __builtin_amdgcn_perm(a[i + 4], a[i], 0x07060302u);  // halves 1
+        a[i] = lo;
+        a[i + 4] = hi;
+    }
+    constexpr int kByteRows[4] = {0, 1, 4, 5};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int i = kByteRows[q];
+        const uint32_t x = __builtin_amdgcn_perm(a[i + 2], a[i], 0x06020400u);  // bytes 0, 2 of a[i], a[i+2]
+        const uint32_t y = __builtin_amdgcn_perm(a[i + 2], a[i], 0x07030501u);  // bytes 1, 3
+        a[i] = x;
+        a[i + 2] = y;
+    }
+    constexpr uint32_t m = 0x0f0f0f0fu;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        const uint32_t x = (a[i] & m) | ((a[i + 1] << 4) & ~m);
+        const uint32_t y = ((a[i] >> 4) & m) | (a[i + 1] & ~m);
+        a[i] = x;
+        a[i + 1] = y;
+    }
+}
+
+// GPTQ qweight [K/8, N] -> MARLIN through the act-order permutation.  A
+// column block of NB columns is repacked over the whole K at once, so every
+// source word is read from HBM once whatever the permutation.  The block's
+// columns are taken in NW = NB / 8 strided groups: group g holds columns
+// g, g + NW, ..., g + 7 NW.
+//   Staging.  A thread loads the 8 source words of one group in one source
+//   row (4-byte loads; the NW threads of a row read NW * 4 contiguous bytes
+//   per load), transposes the 8 x 8 nibbles so that each word holds the
+//   group's 8 columns at one K, and stores the 8 words of K 8r..8r+7 to LDS:
+//   S[g][k], nibble c = column g + NW c at K k; row K holds nibble 8 for the
+//   padding.  The permutation is staged once, as 16-bit entries clamped to
+//   [0, K) with padding entries pointing at row K (PG: too long for LDS beside
+//   the words; the gather reads it from global memory).
+//   Gather.  A thread takes one 32-K tile of one group: 32 LDS reads of
+//   S[g][perm[k]] give the tile's 32 K positions for 8 columns, and four 8 x 8
+//   transposes turn them into the 8 columns' MARLIN words (word tg takes K
+//   offsets 8p + 2tg for p < 4 and 8(p-4) + 2tg + 1 above, as its nibble p).
+//   Store c of the NW threads of a tile then writes columns NW c .. NW c +
+//   NW - 1, NW * 16 contiguous bytes: with adjacent columns per group, each
+//   store would put 16 bytes in each of 64 lines, which measured twice as slow
+//   as the whole write at full lines.
+// Workgroups are persistent and walk column blocks gridDim.x apart; those of
+// one XCD (dispatch assigns workgroup i to XCD i % 8) take adjacent blocks, so
+// the parts of a source line are fetched into one L2.
+// VEC: 16-byte aligned perm (and, for adjacent-column groups, rows).  IT:
+// staging items a thread loads per batch, all in flight before the first is
+// stored.
 constexpr int kPermThreads = 512;
-template <int NB, bool VEC>
+template <int NB, bool VEC, bool PG, int IT>
 __global__ __launch_bounds__(kPermThreads) void repack_gptq_perm_kernel(const uint32_t* __restrict__ qweight,
                                                                         const int32_t* __restrict__ perm,
                                                                         uint32_t* __restrict__ wm, int N, int K,
-                                                                        int nchunks) {
-    static_assert(NB % 4 == 0, "4 columns per thread");
+                                                                        int nchunks, int nblocks) {
+    static_assert(NB % 8 == 0, "8-column groups");
+    constexpr int NW = NB / 8;
+    // strided groups from 32 columns (NW * 4 contiguous bytes per load and
+    // NW * 16 per store); below, groups of adjacent columns, loaded 16 bytes
+    // at a time, read faster than 4- or 8-byte runs
+    constexpr bool SG = NB >= 32;
+    auto col = [&](int blk, int g, int c) { return blk * NB + (SG ? g + NW * c : 8 * g + c); };
     extern __shared__ __attribute__((aligned(16))) uint32_t lds_words[];
-    const int k8 = K >> 3;
-    uint32_t* sq = lds_words;                                      // [K/8][NB]
-    uint16_t* sp = reinterpret_cast<uint16_t*>(lds_words + k8 * NB);  // [Kpad]
+    const int rs = K + 4;  // words per column group: K rows, the padding row, 16-byte alignment
+    uint16_t* sp = reinterpret_cast<uint16_t*>(lds_words + NW * rs);  // [kpad], unless PG
     const int kpad = nchunks * 64;
-    const int n0 = blockIdx.x * NB;
-    // staging, kStage loads in flight per thread before their LDS stores (a
-    // store right behind its load would make every step a memory round trip)
-    constexpr int kStage = 8;
-    constexpr int kQuadsPerRow = NB / 4;
-    const u32x4 pad4 = u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};  // padding: nibble 8
-    for (int i0 = threadIdx.x; i0 < k8 * kQuadsPerRow; i0 += kPermThreads * kStage) {
-        u32x4 v[kStage];
-#pragma unroll
-        for (int q = 0; q < kStage; ++q) {
-            const int i = i0 + q * kPermThreads;
-            const int r = i / kQuadsPerRow, c = (i % kQuadsPerRow) * 4;
-            const uint32_t* src = qweight + (int64_t)r * N + n0 + c;
-            v[q] = pad4;
-            if (i < k8 * kQuadsPerRow) {
-                if (VEC && n0 + c + 3 < N) {
-                    v[q] = *reinterpret_cast<const u32x4*>(src);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (n0 + c + e < N) v[q][e] = src[e];
-                }
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < kStage; ++q) {
-            const int i = i0 + q * kPermThreads;
-            if (i < k8 * kQuadsPerRow) *reinterpret_cast<u32x4*>(sq + (int64_t)i * 4) = v[q];
-        }
-    }
-    // padding rows (k >= K) point at row 0 and are masked below
-    for (int k0 = threadIdx.x * 4; k0 < kpad; k0 += kPermThreads * 4 * kStage) {
-        u32x4 v[kStage];
-#pragma unroll
-        for (int q = 0; q < kStage; ++q) {
-            const int k = k0 + q * kPermThreads * 4;
-            v[q] = u32x4{0u, 0u, 0u, 0u};
-            if (k < K) {  // K % 4 == 0: whole vectors
-                if constexpr (VEC) {
-                    v[q] = *reinterpret_cast<const u32x4*>(perm + k);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[q][e] = (uint32_t)perm[k + e];
-                }
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < kStage; ++q) {
-            const int k = k0 + q * kPermThreads * 4;
-            if (k < kpad) {
-                uint32_t p2[2];
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    // clamped: a bad perm cannot fault
-                    const uint32_t a = (uint32_t)min(max((int)v[q][2 * h], 0), K - 1);
-                    const uint32_t b = (uint32_t)min(max((int)v[q][2 * h + 1], 0), K - 1);
-                    p2[h] = a | (b << 16);
-                }
-                *reinterpret_cast<u32x2*>(sp + k) = u32x2{p2[0], p2[1]};
-            }
-        }
-    }
-    __syncthreads();
-    constexpr int kQuads = NB / 4;  // threads per tile
     const int ktiles = nchunks * 2;
-    // Each gathered nibble goes straight to its MARLIN place: K offset 8j + e of
-    // the tile (run j, entry e) is nibble j + 4 (e % 2) of word e / 2 -- the
-    // word transpose_tile_bytes would build from source run j's byte e / 2.
-    for (int i = threadIdx.x; i < ktiles * kQuads; i += kPermThreads) {
-        const int t = i / kQuads, c0 = (i % kQuads) * 4;
-        uint32_t out[4][4] = {};  // [column q][MARLIN word tg]
+    const int nitems = (K >> 3) * NW;  // staging items of a block
+    const int grid = gridDim.x;
+    const int first = (grid & 7) == 0 ? (int)(blockIdx.x & 7) * (grid >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+    if (first >= nblocks) return;
+    const int tid = threadIdx.x;
+
+    // Block blk into LDS.  Every load is issued, from a clamped address where
+    // the item or its column is out of range, and the padding selected when
+    // the words are stored: a load inside a divergent branch is waited for
+    // where the branch joins, one at a time.
+    auto stage = [&](int blk) {
+        for (int i0 = tid; i0 < nitems; i0 += IT * kPermThreads) {
+            uint32_t v[IT][8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int kb = t * 32 + j * 8;
-            if (kb >= K) {  // padding rows (K % 8 == 0: whole runs): nibble 8
+            for (int q = 0; q < IT; ++q) {
+                const int i = i0 + q * kPermThreads;
+                const bool ok = i < nitems;
+                const uint32_t* row = qweight + (ok ? (int64_t)(i / NW) * N : 0);
+                const int g = i % NW;
+                if constexpr (!SG && VEC) {  // adjacent columns: two 16-byte loads
+                    const int c0 = col(blk, g, 0);
+                    const u32x4 a = *reinterpret_cast<const u32x4*>(ok && c0 + 3 < N ? row + c0 : qweight);
+                    const u32x4 b = *reinterpret_cast<const u32x4*>(ok && c0 + 7 < N ? row + c0 + 4 : qweight);
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
+                    for (int c = 0; c < 4; ++c) {
+                        v[q][c] = a[c];
+                        v[q][c + 4] = b[c];
+                    }
+                } else {
 #pragma unroll
-                    for (int tg = 0; tg < 4; ++tg) out[q][tg] |= (8u << (4 * j)) | (8u << (4 * j + 16));
-                continue;
+                    for (int c = 0; c < 8; ++c) {
+                        const int n = col(blk, g, c);
+                        v[q][c] = *(ok && n < N ? row + n : qweight);
+                    }
+                }
             }
-            const u32x4 pk = *reinterpret_cast<const u32x4*>(sp + kb);  // 8 permutation entries
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int sk = (pk[e >> 1] >> (16 * (e & 1))) & 0xffff;
-                const u32x4 row = *reinterpret_cast<const u32x4*>(sq + (sk >> 3) * NB + c0);
-                const int sh = 4 * (sk & 7);
+            for (int q = 0; q < IT; ++q) {
+                const int i = i0 + q * kPermThreads;
+                if (i < nitems) {
+                    const int g = i % NW;
+                    uint32_t a[8];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) out[q][e >> 1] |= ((row[q] >> sh) & 0xfu) << (4 * j + 16 * (e & 1));
+                    for (int c = 0; c < 8; ++c) {
+                        // 16-byte loads take whole 4-column quads (N % 4 == 0)
+                        const int n = !SG && VEC ? col(blk, g, c & 4) + 3 : col(blk, g, c);
+                        a[c] = n < N ? v[q][c] : 0x88888888u;
+                    }
+                    transpose_nibbles8(a);
+                    uint32_t* dst = lds_words + g * rs + (i / NW) * 8;
+                    *reinterpret_cast<u32x4*>(dst) = u32x4{a[0], a[1], a[2], a[3]};
+                    *reinterpret_cast<u32x4*>(dst + 4) = u32x4{a[4], a[5], a[6], a[7]};
+                }
             }
         }
+    };
+    // Block blk from LDS to the MARLIN words.
+    auto gather = [&](int blk) {
+        for (int i = tid; i < ktiles * NW; i += kPermThreads) {
+            const int t = i / NW, w = i % NW;
+            const uint32_t* grp = lds_words + w * rs;
+            uint32_t g[32];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            *reinterpret_cast<u32x4*>(wm + marlin_offset(n0 + c0 + q, t, nchunks)) =
-                u32x4{out[q][0], out[q][1], out[q][2], out[q][3]};
+            for (int h = 0; h < 4; ++h) {
+                const int kb = t * 32 + h * 8;
+                uint32_t sk[8];
+                if constexpr (PG) {
+                    u32x4 p[2];
+                    const int kc = kb < K ? kb : 0;  // unconditional loads, as in the staging
+                    if constexpr (VEC) {
+                        p[0] = *reinterpret_cast<const u32x4*>(perm + kc);
+                        p[1] = *reinterpret_cast<const u32x4*>(perm + kc + 4);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) p[e >> 2][e & 3] = (uint32_t)perm[kc + e];
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        sk[e] = kb < K ? (uint32_t)min(max((int)p[e >> 2][e & 3], 0), K - 1) : (uint32_t)K;
+                } else {
+                    const u32x4 pk = *reinterpret_cast<const u32x4*>(sp + kb);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) sk[e] = (pk[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) g[8 * h + e] = grp[sk[e]];
+            }
+            uint32_t out[4][8];
+#pragma unroll
+            for (int tg = 0; tg < 4; ++tg) {
+#pragma unroll
+                for (int p = 0; p < 8; ++p) out[tg][p] = g[8 * (p & 3) + 2 * tg + (p >> 2)];
+                transpose_nibbles8(out[tg]);
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                *reinterpret_cast<u32x4*>(wm + marlin_offset(col(blk, w, c), t, nchunks)) =
+                    u32x4{out[0][c], out[1][c], out[2][c], out[3][c]};
         }
+    };
+
+    // the permutation, once for all blocks
+    if constexpr (!PG) {
+        for (int k = tid * 4; k < kpad; k += kPermThreads * 4) {
+            u32x4 p = u32x4{0u, 0u, 0u, 0u};
+            const int kc = k < K ? k : 0;  // K % 8 == 0: whole vectors
+            if constexpr (VEC) {
+                p = *reinterpret_cast<const u32x4*>(perm + kc);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) p[e] = (uint32_t)perm[kc + e];
+            }
+            uint32_t e4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)  // clamped: a bad perm cannot fault
+                e4[e] = k < K ? (uint32_t)min(max((int)p[e], 0), K - 1) : (uint32_t)K;
+            *reinterpret_cast<u32x2*>(sp + k) = u32x2{e4[0] | (e4[1] << 16), e4[2] | (e4[3] << 16)};
+        }
+    }
+    if (tid < NW) lds_words[tid * rs + K] = 0x88888888u;
+    for (int blk = first; blk < nblocks; blk += grid) {
+        stage(blk);
+        __syncthreads();
+        gather(blk);
+        __syncthreads();
     }
 }
 
@@ -350,47 +430,82 @@ hipError_t launch_repack_ct(const uint32_t* packed, const void* ws, int stype_in
 }
 
 namespace {
-template <int NB>
+template <int NB, int IT>
 hipError_t launch_repack_gptq_perm(const uint32_t* qweight, const int32_t* perm, uint32_t* wm, int N, int K,
-                                   int npad, int kpad, size_t lds, hipStream_t stream, hipEvent_t start,
-                                   hipEvent_t stop) {
-    // 16-byte staging loads: 4-column quads of a row and 4-entry runs of perm aligned
-    const bool vec = N % 4 == 0 && ((reinterpret_cast<uintptr_t>(qweight) | reinterpret_cast<uintptr_t>(perm)) & 15) == 0;
-    const auto fn = vec ? repack_gptq_perm_kernel<NB, true> : repack_gptq_perm_kernel<NB, false>;
+                                   int npad, int kpad, size_t lds, bool pg, int grid, hipStream_t stream,
+                                   hipEvent_t start, hipEvent_t stop) {
+    // 16-byte loads: 4-entry runs of perm, and (adjacent-column groups) 4-column quads of a row
+    const bool vec = (reinterpret_cast<uintptr_t>(perm) & 15) == 0 &&
+                     (NB >= 32 || (N % 4 == 0 && (reinterpret_cast<uintptr_t>(qweight) & 15) == 0));
+    auto pick = [&]() {
+        if constexpr (NB == 8) {  // the permutation from global memory only at 8 columns
+            if (pg) return vec ? repack_gptq_perm_kernel<NB, true, true, IT> : repack_gptq_perm_kernel<NB, false, true, IT>;
+        }
+        return vec ? repack_gptq_perm_kernel<NB, true, false, IT> : repack_gptq_perm_kernel<NB, false, false, IT>;
+    };
+    const auto fn = pick();
     if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    launch_kernel(fn, dim3(npad / NB), dim3(kPermThreads), (uint32_t)lds, stream, start, stop, qweight, perm, wm, N,
-                  K, kpad / kMarlinBK);
+    launch_kernel(fn, dim3(grid), dim3(kPermThreads), (uint32_t)lds, stream, start, stop, qweight, perm, wm, N, K,
+                  kpad / kMarlinBK, npad / NB);
     return hipGetLastError();
 }
 }  // namespace
 
 hipError_t launch_repack_gptq(const uint32_t* qweight, const int32_t* perm, uint32_t* wm, int N, int K,
-                              hipStream_t stream, hipEvent_t start, hipEvent_t stop, int cus) {
+                              hipStream_t stream, hipEvent_t start, hipEvent_t stop, int cus, int cols_override,
+                              int grid_override) {
     const int npad = (int)round_up(N, kMarlinBN), kpad = (int)round_up(K, kMarlinBK);
     if (npad == 0 || kpad == 0) return hipSuccess;
     if (perm != nullptr && K <= 65535) {
-        // act-order through LDS: the widest column block whose source words and
-        // permutation fit and that still gives every CU a workgroup, else the
-        // narrowest that fits
+        // act-order through LDS: the widest block (64 or 32 columns in strided
+        // groups, else 16 or 8 adjacent) whose words and permutation fit and
+        // whose blocks cover at least half the CUs, else the narrowest that
+        // fits; past that, 8 columns with the permutation read from global
+        // memory.  One workgroup per block up to two blocks per CU, else one
+        // persistent workgroup per CU.  Measured on MI355X, kernel only, us:
+        // Llama-3-8B gate 15.0 at 64 columns (20.3-21.0 at 32), q 7.4 at 32
+        // (8.1 at 64), k 4.9 at 8 (6.3 at 32), down 24.1 at 16 (the widest
+        // that fits K = 14336); 70B qkv 31.2 with 320 workgroups (37.9 with
+        // 256 walking 1.25 blocks each), gate_up 132 with 256 persistent
+        // workgroups (138 with 512).
         constexpr size_t kLdsCap = 152 * 1024;
+        auto words_bytes = [&](int w) { return (size_t)(w / 8) * (K + 4) * 4; };
+        const size_t perm_bytes = (size_t)kpad * 2;
+        auto fits = [&](int w) { return words_bytes(w) + perm_bytes <= kLdsCap; };
         int nb = 0;
-        for (int w : {64, 32, 16, 8, 4}) {
-            const size_t lds = (size_t)(K / 8) * w * 4 + (size_t)kpad * 2;
-            if (lds > kLdsCap) continue;
-            nb = w;
-            if (npad / w >= cus) break;
+        bool pg = false;
+        if (cols_override != 0 && fits(cols_override)) {
+            nb = cols_override;
+        } else {
+            for (int w : {64, 32, 16, 8}) {
+                if (!fits(w)) continue;
+                nb = w;
+                if (2 * (npad / w) >= cus) break;
+            }
+        }
+        if (nb == 0 && words_bytes(8) <= kLdsCap) {
+            nb = 8;
+            pg = true;
         }
         if (nb != 0) {
-            const size_t lds = (size_t)(K / 8) * nb * 4 + (size_t)kpad * 2;
-            switch (nb) {
-                case 64: return launch_repack_gptq_perm<64>(qweight, perm, wm, N, K, npad, kpad, lds, stream, start, stop);
-                case 32: return launch_repack_gptq_perm<32>(qweight, perm, wm, N, K, npad, kpad, lds, stream, start, stop);
-                case 16: return launch_repack_gptq_perm<16>(qweight, perm, wm, N, K, npad, kpad, lds, stream, start, stop);
-                case 8: return launch_repack_gptq_perm<8>(qweight, perm, wm, N, K, npad, kpad, lds, stream, start, stop);
-                default: return launch_repack_gptq_perm<4>(qweight, perm, wm, N, K, npad, kpad, lds, stream, start, stop);
+            const size_t lds = words_bytes(nb) + (pg ? 0 : perm_bytes);
+            const int nblocks = npad / nb;
+            const int grid = grid_override > 0 ? std::min(nblocks, grid_override)
+                                               : (nblocks <= 2 * cus ? nblocks : cus);
+            // four staging items per thread cover a block of K * NB <= 4 * 64 * 512 (K = 4096 at 32 columns)
+            const bool it8 = (int64_t)(K / 8) * (nb / 8) > 4 * kPermThreads;
+            switch (nb * (it8 ? -1 : 1)) {
+                case 64: return launch_repack_gptq_perm<64, 4>(qweight, perm, wm, N, K, npad, kpad, lds, pg, grid, stream, start, stop);
+                case -64: return launch_repack_gptq_perm<64, 8>(qweight, perm, wm, N, K, npad, kpad, lds, pg, grid, stream, start, stop);
+                case 32: return launch_repack_gptq_perm<32, 4>(qweight, perm, wm, N, K, npad, kpad, lds, pg, grid, stream, start, stop);
+                case -32: return launch_repack_gptq_perm<32, 8>(qweight, perm, wm, N, K, npad, kpad, lds, pg, grid, stream, start, stop);
+                case 16: return launch_repack_gptq_perm<16, 4>(qweight, perm, wm, N, K, npad, kpad, lds, pg, grid, stream, start, stop);
+                case -16: return launch_repack_gptq_perm<16, 8>(qweight, perm, wm, N, K, npad, kpad, lds, pg, grid, stream, start, stop);
+                case 8: return launch_repack_gptq_perm<8, 4>(qweight, perm, wm, N, K, npad, kpad, lds, pg, grid, stream, start, stop);
+                default: return launch_repack_gptq_perm<8, 8>(qweight, perm, wm, N, K, npad, kpad, lds, pg, grid, stream, start, stop);
             }
         }
     }

@@ -197,9 +197,12 @@ hipError_t launch_gather_x(const uint16_t* x, const int32_t* perm, uint16_t* out
 hipError_t launch_repack_ct(const uint32_t* packed, const void* ws, int stype_in, uint32_t* wm, float* sm, int N,
                             int K, int G, hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 // perm (act-order) takes an LDS-staged kernel sized by `cus`, the device's CU count.
+// cols_override / grid_override (tuning sweeps and tests; 0 = heuristic): the
+// act-order kernel's column block width (8, 16, 32 or 64) and its number of
+// workgroups (each walks the blocks gridDim.x apart).
 hipError_t launch_repack_gptq(const uint32_t* qweight, const int32_t* perm, uint32_t* wm, int N, int K,
                               hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr,
-                              int cus = 256);
+                              int cus = 256, int cols_override = 0, int grid_override = 0);
 hipError_t launch_gidx_perm(const int32_t* g_idx, int32_t* perm, int32_t* status, int K, int G, hipStream_t stream);
 
 }  // namespace pw4

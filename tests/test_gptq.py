@@ -4,6 +4,8 @@ GEMM vs the fp32 oracle of w = (u - z[g_idx[k]]) * s[g_idx[k]].  The reference
 has no zero points and no act-order, so these are pinned by the oracle and by
 invariants (symmetric GPTQ == compressed-tensors repack, bytewise)."""
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -25,9 +27,9 @@ def test_symmetric_gptq_equals_reference_repack(n, k):
 
 
 # The act-order repack stages a column block's source words and the permutation in LDS,
-# 4 to 64 columns wide by K and N: the shapes below take every width (K up to 28672),
-# ragged N and K tails; N % 4 != 0 (130, 66) takes the word-by-word staging path, the
-# others 16-byte staging loads.
+# 8 to 64 columns wide by K and N: the shapes below take every width (K up to 28672, where
+# the permutation is read from global memory), ragged N and K tails; N % 4 != 0 (130, 66)
+# takes the word-by-word staging path at 8 and 16 columns.
 @pytest.mark.parametrize("n,k,g", [(256, 1024, 128), (136, 512, 64), (64, 256, 32), (128, 4096, 128),
                                    (200, 2112, 64), (14336, 4096, 128), (4096, 4096, 128),
                                    (1024, 4096, 128), (4096, 14336, 128), (512, 28672, 128), (16384, 4096, 128),
@@ -41,6 +43,31 @@ def test_act_order_repack_bit_exact(n, k, g):
     assert np.array_equal(perm.cpu().numpy(), want_perm)
     assert np.array_equal(perm.cpu().numpy(), np.argsort(c.g_idx, kind="stable"))
     want = O.repack_gptq_marlin(O.pack_gptq(c.u), want_perm)
+    assert np.array_equal(wm.cpu().numpy(), want)
+
+
+# Every column block width on ragged N, each with the workgroups walking several blocks
+# (grid 1 and 3) and one block each: 32 and 64 columns take the strided column groups
+# (columns g, g + NW, ...), 8 and 16 the adjacent ones; N = 130 the word-by-word loads.
+@pytest.mark.parametrize("n,k", [(200, 1024), (130, 512)])
+@pytest.mark.parametrize("cols", [8, 16, 32, 64])
+@pytest.mark.parametrize("grid", [1, 3, 0])
+def test_act_order_repack_widths_and_grids(n, k, cols, grid):
+    c = baseline_case(1, n, k, 64, seed=5, symmetric=True, act_order=True)
+    g_idx = torch.from_numpy(c.g_idx).cuda()
+    want = O.repack_gptq_marlin(O.pack_gptq(c.u), O.gidx_perm(c.g_idx, 64))
+    keys = ("PW4_REPACK_COLS", "PW4_REPACK_GRID")
+    old = {key: os.environ.get(key) for key in keys}
+    os.environ["PW4_REPACK_COLS"] = str(cols)
+    os.environ["PW4_REPACK_GRID"] = str(grid)
+    try:
+        wm, _ = ops.repack_w4a16_gptq(c.qweight(), g_idx, 64)
+    finally:
+        for key, v in old.items():
+            if v is None:
+                os.environ.pop(key, None)
+            else:
+                os.environ[key] = v
     assert np.array_equal(wm.cpu().numpy(), want)
 
 
