@@ -167,12 +167,11 @@ def cpu_baseline() -> dict:
       value  - configs[1], the 16 decode-sweep GEMMs: bytes over the summed
                per-call times (dequant and GEMM each a median of 5), GB/s;
       config1_m1_k4096_n4096 - configs[0], its two phases apart (median of 5);
-      prefill - configs[2]: GEMM at M = 256 and 1024 (median of 3 / 1) and at
-                M = 4096 timed on 1024 rows and scaled by 4 (rows of a GEMM
-                cost alike), plus the layer's dequant;
+      prefill - configs[2]: GEMM at M = 256, 1024 and 4096 (median of 3 /
+                once / once), plus the layer's dequant;
       act_order_70b - configs[3]: the asymmetric act-order dequant of each 70B
                 layer (once), GEMM at M = 1, 16 (median of 3) and at M = 2048
-                timed on 256 rows and scaled by 8;
+                (once);
       stack  - configs[4]: one Llama-3-8B layer's seven linears at M = 1 and
                32 (median of 3 each phase) times 32 layers (the layers have
                the same shapes), per decode token."""
@@ -234,7 +233,7 @@ def cpu_baseline() -> dict:
     prefill = {}
     for name, k, n in LLAMA8B:
         w, dq = l8[name]
-        for m, rows, reps in ((256, 256, 3), (1024, 1024, 1), (4096, 1024, 1)):
+        for m, rows, reps in ((256, 256, 3), (1024, 1024, 1), (4096, 4096, 1)):
             gm = gemm_time(w, rows, reps) * (m // rows)
             prefill[f"{name}_m{m}"] = {"dequant_ms": round(dq * 1e3, 2), "gemm_ms": round(gm * 1e3, 2),
                                        "total_ms": round((dq + gm) * 1e3, 2),
@@ -244,14 +243,13 @@ def cpu_baseline() -> dict:
     for name, k, n in LLAMA70B:
         w, dq = l70[name]
         res = {"dequant_ms": round(dq * 1e3, 1)}
-        for m, rows, reps in ((1, 1, 3), (16, 16, 3), (2048, 256, 1)):
+        for m, rows, reps in ((1, 1, 3), (16, 16, 3), (2048, 2048, 1)):
             gm = gemm_time(w, rows, reps) * (m // rows)
             r = {"gemm_ms": round(gm * 1e3, 2), "total_ms": round((dq + gm) * 1e3, 1)}
             if m <= 16:
                 r["GB/s"] = round(act_order_bytes(m, k, n) / (dq + gm) / 1e9, 3)
             else:
                 r["TFLOP/s"] = round(2.0 * m * n * k / (dq + gm) / 1e12, 4)
-                r["gemm_rows_timed"] = rows
             res[f"m{m}"] = r
         act[name] = res
     del l70
@@ -276,10 +274,9 @@ def cpu_baseline() -> dict:
         "prefill": prefill,
         "act_order_70b": act,
         "stack": stack,
-        "notes": {"prefill": "per layer: dequant median of 5; GEMM M=256 median of 3, M=1024 once, M=4096 timed "
-                             "on 1024 rows x 4",
+        "notes": {"prefill": "per layer: dequant median of 5; GEMM M=256 median of 3, M=1024 and M=4096 once",
                   "act_order_70b": "asymmetric act-order dequant (zero points, g_idx) once per layer; GEMM M=1, 16 "
-                                   "median of 3, M=2048 timed on 256 rows x 8",
+                                   "median of 3, M=2048 once",
                   "stack": "one layer's 7 linears (dequant median of 5, GEMM median of 3) x 32 layers"},
         "cpu_seconds": round(time.perf_counter() - t_start, 1),
     }
