@@ -572,7 +572,12 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         // The CT layout (gemm_w4a16) reaches the 256-wide kernel through a
         // per-call repack into the workspace: one pass over the weights
         // (~5 us for 4096 x 4096) against the 128 x 128 kernel's ~2x slower
-        // GEMM at every M past the decode range.
+        // GEMM at every M past the decode range.  At M = 33..64 it also beats
+        // decode calls over 32-row blocks on every Llama-3 8B and 70B layer
+        // but 8B o (graph periods, us, M = 33 and 64, this plan / 128 x 128
+        // on CT / decode blocks: 8B gate_up 64.4 and 66.2 / 109 and 109 /
+        // 70.2 and 83.4, 70B down 113 and 114 / 271 and 275 / 216 and 346;
+        // 8B o 27.1 and 27.4 / 30.7 and 33.5 / 22.8 and 26.3).
         if (p.p256 && layout == LAYOUT_CT) {
             p.repack_bytes = align_up((size_t)round_up(N, kMarlinBN) * round_up(K, kMarlinBK) / 2) +
                              (size_t)(K / G) * N * sizeof(float);
