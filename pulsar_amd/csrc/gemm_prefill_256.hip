@@ -40,7 +40,8 @@
 //
 // Exact scaling (fp16 x, the default).  Rounding (u - z) * s to fp16 costs up
 // to 2^-11 of every weight; summed over K = 14336-28672 that is ~1e-2 of
-// absolute error at the BASELINE magnitudes.  In this mode B = u - z (exact in
+// absolute error for x ~ N(0, 1) and scales ~ |N(0, 0.02)| (the benchmark's
+// Llama-3 distributions).  In this mode B = u - z (exact in
 // fp16) and the group scale is applied in fp32 to the accumulators instead:
 // with s_g the scale of group g for the lane's column, the running sum is
 // rescaled by s_(g-1) / s_g when group g starts and multiplied by the last
