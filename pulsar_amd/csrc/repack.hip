@@ -193,7 +193,9 @@ __device__ __forceinline__ void transpose_nibbles8(uint32_t (&a)[8]) {
 //   Store c of the NW threads of a tile then writes columns NW c .. NW c +
 //   NW - 1, NW * 16 contiguous bytes: with adjacent columns per group, each
 //   store would put 16 bytes in each of 64 lines, which measured twice as slow
-//   as the whole write at full lines.
+//   as the whole write at full lines.  At 16 columns the groups are adjacent
+//   (for 16-byte loads), and the tile's two threads swap half their words
+//   before storing, so that their stores pair up into 32-byte runs.
 // Workgroups are persistent and walk column blocks gridDim.x apart; those of
 // one XCD (dispatch assigns workgroup i to XCD i % 8) take adjacent blocks, so
 // the parts of a source line are fetched into one L2.
@@ -312,10 +314,39 @@ __global__ __launch_bounds__(kPermThreads) void repack_gptq_perm_kernel(const ui
                 for (int p = 0; p < 8; ++p) out[tg][p] = g[8 * (p & 3) + 2 * tg + (p >> 2)];
                 transpose_nibbles8(out[tg]);
             }
+            if constexpr (!SG && NW == 2) {
+                // 16 columns: lanes 2j and 2j + 1 hold columns 0-7 and 8-15 of
+                // one tile.  They swap four words (the first lane's odd columns
+                // for the second's even ones, DPP quad_perm [1, 0, 3, 2]), so that
+                // store c of the pair writes columns 2c and 2c + 1: 32 contiguous
+                // bytes instead of 16 bytes in each of two lines.
+                uint32_t recv[4][4];
 #pragma unroll
-            for (int c = 0; c < 8; ++c)
-                *reinterpret_cast<u32x4*>(wm + marlin_offset(col(blk, w, c), t, nchunks)) =
-                    u32x4{out[0][c], out[1][c], out[2][c], out[3][c]};
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int tg = 0; tg < 4; ++tg) {
+                        const uint32_t send = w ? out[tg][2 * j] : out[tg][2 * j + 1];
+                        recv[j][tg] = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xF, 0xF, true);
+                    }
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    u32x4 v;
+#pragma unroll
+                    for (int tg = 0; tg < 4; ++tg) {
+                        if (c < 4) {
+                            v[tg] = w ? recv[c][tg] : out[tg][2 * c];
+                        } else {
+                            v[tg] = w ? out[tg][2 * c - 7] : recv[c - 4][tg];
+                        }
+                    }
+                    *reinterpret_cast<u32x4*>(wm + marlin_offset(blk * NB + 2 * c + w, t, nchunks)) = v;
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    *reinterpret_cast<u32x4*>(wm + marlin_offset(col(blk, w, c), t, nchunks)) =
+                        u32x4{out[0][c], out[1][c], out[2][c], out[3][c]};
+            }
         }
     };
 
