@@ -231,6 +231,55 @@ __global__ __launch_bounds__(kPermThreads) void repack_gptq_perm_kernel(const ui
     // the words are stored: a load inside a divergent branch is waited for
     // where the branch joins, one at a time.
     auto stage = [&](int blk) {
+        if constexpr (!SG && VEC && NW == 2) {
+            // 16 columns, one 64-byte run per row: lane l of a wave loads the
+            // 16-byte quad 4 (l % 4) of rows r0 + l / 4 and r0 + l / 4 + 16
+            // (four lanes per run).  Lanes 2j and 2j + 1 then swap one row's
+            // quads through DPP, so that the first holds both quads of group
+            // (l % 4) / 2 in the first row and the second in the other row: the
+            // wave's 64 items (32 rows x 2 groups), as in the loop below.  The
+            // loop runs by whole waves, since a lane's partner must be active.
+            const int lane = tid & 63, p = lane & 3, g = p >> 1;
+            const bool second = (p & 1) != 0;
+            const int nrows = K >> 3;
+            const int c0 = blk * NB + 4 * p;  // this lane's quad
+            for (int base = tid & ~63; base < nitems; base += IT * kPermThreads) {
+                u32x4 va[IT], vb[IT];
+#pragma unroll
+                for (int q = 0; q < IT; ++q) {
+                    const int ra = ((base + q * kPermThreads) >> 1) + (lane >> 2), rb = ra + 16;
+                    va[q] = *reinterpret_cast<const u32x4*>(ra < nrows && c0 + 3 < N ? qweight + (int64_t)ra * N + c0
+                                                                                      : qweight);
+                    vb[q] = *reinterpret_cast<const u32x4*>(rb < nrows && c0 + 3 < N ? qweight + (int64_t)rb * N + c0
+                                                                                      : qweight);
+                }
+#pragma unroll
+                for (int q = 0; q < IT; ++q) {
+                    const int ra = ((base + q * kPermThreads) >> 1) + (lane >> 2);
+                    const int r = second ? ra + 16 : ra;
+                    uint32_t a[8];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t send = second ? va[q][e] : vb[q][e];
+                        const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xF, 0xF, true);
+                        a[e] = second ? recv : va[q][e];
+                        a[e + 4] = second ? vb[q][e] : recv;
+                    }
+                    if (r < nrows) {
+#pragma unroll
+                        for (int c = 0; c < 8; ++c) {
+                            // whole 4-column quads (N % 4 == 0)
+                            if (col(blk, g, c & 4) + 3 >= N) a[c] = 0x88888888u;
+                        }
+                        transpose_nibbles8(a);
+                        uint32_t* dst = lds_words + g * rs + r * 8;
+                        *reinterpret_cast<u32x4*>(dst) = u32x4{a[0], a[1], a[2], a[3]};
+                        *reinterpret_cast<u32x4*>(dst + 4) = u32x4{a[4], a[5], a[6], a[7]};
+                    }
+                }
+            }
+            return;
+        }
         for (int i0 = tid; i0 < nitems; i0 += IT * kPermThreads) {
             uint32_t v[IT][8];
 #pragma unroll
