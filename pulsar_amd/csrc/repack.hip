@@ -429,50 +429,65 @@ __global__ __launch_bounds__(kPermThreads) void repack_gptq_perm_kernel(const ui
 // perm = stable argsort(g_idx) for an act-order checkpoint: one workgroup per
 // group collects, in ascending k, the rows that belong to it.  status bit 0:
 // some group does not hold exactly G rows; bit 1: a group id out of range.
-// The entries are ranked 256 at a time in k order (ballot and popcount within a
-// wave, counts of the earlier waves through LDS); a thread loads its entries of
-// kGidxBatch such steps at once, so a step costs one barrier rather than a
-// memory round trip, and the wave counts are double buffered so that one
-// barrier per step suffices.
+// Wave w of the workgroup takes the w-th quarter of k (whole 64-entry steps).
+// Pass 1: each wave counts its rows of the group, 64 entries per ballot, with
+// no barrier.  One barrier hands the four counts over.  Pass 2: each wave
+// walks its quarter again and writes row k at the group's count of earlier
+// rows (earlier waves, earlier steps, lower lanes).  A lane loads its entries
+// of kGidxBatch steps at once, so the walk costs a memory round trip per
+// kGidxBatch steps.
 constexpr int kGidxBatch = 16;
 __global__ __launch_bounds__(256) void gidx_perm_kernel(const int32_t* __restrict__ g_idx, int32_t* __restrict__ perm,
                                                         int32_t* __restrict__ status, int K, int G) {
-    __shared__ int wave_cnt[2][4];
+    __shared__ int wave_cnt[4];
     const int g = blockIdx.x;
     const int Kg = K / G;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    int base_count = 0;
-    int buf = 0;
-    for (int kb = 0; kb < K; kb += 256 * kGidxBatch) {
+    const int quarter = ((K + 255) / 256) * 64;  // entries per wave, a multiple of 64
+    const int k_begin = wave * quarter, k_end = min(k_begin + quarter, K);
+    const uint64_t below = (1ull << lane) - 1ull;
+    // one batch of kGidxBatch steps: the group's rows among entries k0 + 64 b + lane
+    auto batch = [&](int k0, bool (&mine)[kGidxBatch]) {
         int gv[kGidxBatch];
 #pragma unroll
         for (int b = 0; b < kGidxBatch; ++b) {
-            const int k = kb + b * 256 + tid;
-            gv[b] = k < K ? g_idx[k] : -1;
+            const int k = k0 + b * 64 + lane;
+            gv[b] = k < k_end ? g_idx[k] : -1;
         }
 #pragma unroll
         for (int b = 0; b < kGidxBatch; ++b) {
-            const int k = kb + b * 256 + tid;
-            if (kb + b * 256 >= K) break;  // uniform: every thread leaves at the same step
-            if (g == 0 && k < K && (gv[b] < 0 || gv[b] >= Kg)) atomicOr(status, 2);
-            const bool mine = k < K && gv[b] == g;
-            const uint64_t mask = __ballot(mine);
-            const int before_lane = __popcll(mask & ((1ull << lane) - 1ull));
-            if (lane == 0) wave_cnt[buf][wave] = __popcll(mask);
-            __syncthreads();
-            int before_wave = 0, total = 0;
+            const int k = k0 + b * 64 + lane;
+            if (g == 0 && k < k_end && (gv[b] < 0 || gv[b] >= Kg)) atomicOr(status, 2);
+            mine[b] = k < k_end && gv[b] == g;
+        }
+    };
+    int count = 0;
+    for (int k0 = k_begin; k0 < k_end; k0 += 64 * kGidxBatch) {
+        bool mine[kGidxBatch];
+        batch(k0, mine);
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                before_wave += w < wave ? wave_cnt[buf][w] : 0;
-                total += wave_cnt[buf][w];
-            }
-            const int pos = base_count + before_wave + before_lane;
-            if (mine && pos < G) perm[(int64_t)g * G + pos] = k;
-            base_count += total;
-            buf ^= 1;  // the next step writes the other buffer: no barrier before it
+        for (int b = 0; b < kGidxBatch; ++b) count += __popcll(__ballot(mine[b]));
+    }
+    if (lane == 0) wave_cnt[wave] = count;
+    __syncthreads();
+    int pos = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        pos += w < wave ? wave_cnt[w] : 0;
+        total += wave_cnt[w];
+    }
+    for (int k0 = k_begin; k0 < k_end; k0 += 64 * kGidxBatch) {
+        bool mine[kGidxBatch];
+        batch(k0, mine);
+#pragma unroll
+        for (int b = 0; b < kGidxBatch; ++b) {
+            const uint64_t mask = __ballot(mine[b]);
+            const int at = pos + __popcll(mask & below);
+            if (mine[b] && at < G) perm[(int64_t)g * G + at] = k0 + b * 64 + lane;
+            pos += __popcll(mask);
         }
     }
-    if (tid == 0 && base_count != G) atomicOr(status, 1);
+    if (tid == 0 && total != G) atomicOr(status, 1);
 }
 
 __global__ __launch_bounds__(64) void clear_status_kernel(int32_t* __restrict__ status) {

@@ -71,18 +71,19 @@ def test_act_order_repack_widths_and_grids(n, k, cols, grid):
     assert np.array_equal(wm.cpu().numpy(), want)
 
 
-def test_bad_g_idx_rejected():
-    k, g = 256, 64
+@pytest.mark.parametrize("k,g", [(256, 64), (4160, 64), (28672, 128)])
+def test_bad_g_idx_rejected(k, g):
+    """A group with one row too many (and another one short), and a group id out of range,
+    at the first and the last row: each walk of the permutation kernel sees it."""
     g_idx = torch.arange(k, dtype=torch.int32, device="cuda") // g
     qw = torch.zeros(k // 8, 64, dtype=torch.int32, device="cuda")
-    bad = g_idx.clone()
-    bad[0] = 1
-    with pytest.raises(RuntimeError, match="g_idx"):
-        ops.repack_w4a16_gptq(qw, bad, g)
-    bad = g_idx.clone()
-    bad[3] = 99
-    with pytest.raises(RuntimeError, match="g_idx"):
-        ops.repack_w4a16_gptq(qw, bad, g)
+    _, perm = ops.repack_w4a16_gptq(qw, g_idx, g)
+    assert torch.equal(perm.cpu(), torch.arange(k, dtype=torch.int32))
+    for row, value in ((0, 1), (k - 1, 0), (3, k // g + 5), (k - 2, -1)):
+        bad = g_idx.clone()
+        bad[row] = value
+        with pytest.raises(RuntimeError, match="g_idx"):
+            ops.repack_w4a16_gptq(qw, bad, g)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
