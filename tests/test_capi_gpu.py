@@ -125,3 +125,30 @@ def test_workspace_too_small_is_rejected(env):
                                      None) == 0
     out = hip.download(y, (p.m, p.n), np.uint16)
     check(torch.from_numpy(out.view(np.float16)), p.reference(), torch.float16, "C ABI exact workspace")
+
+
+@pytest.mark.parametrize("k,g", [(18, 6), (4096, 128), (4100, 4), (8200, 8), (28672, 128)])
+@pytest.mark.parametrize("offset", [0, 4])
+def test_gidx_to_perm_alignments(k, g, offset):
+    """pw4_gidx_to_perm on a 16-byte aligned g_idx and one 4 bytes past it, at K up to and past
+    4096 (the entry-by-entry walk, and past 4096 the 16-byte loads where aligned), against
+    numpy's stable argsort; then one row moved to another group must set the status word."""
+    lib = declare(pulsar_amd.capi())
+    hip = Hip()
+    try:
+        rng = np.random.default_rng(k + offset)
+        g_idx = rng.permutation(np.arange(k, dtype=np.int32) // g).astype(np.int32)
+        buf = np.concatenate([np.zeros(offset // 4, np.int32), g_idx])
+        base = hip.upload(buf)
+        perm = hip.malloc(k * 4)
+        status = hip.malloc(4)
+        assert lib.pw4_gidx_to_perm(base + offset, k, g, perm, status, None) == 0
+        assert hip.download(status, (1,), np.int32)[0] == 0
+        assert np.array_equal(hip.download(perm, (k,), np.int32), np.argsort(g_idx, kind="stable"))
+        bad = g_idx.copy()
+        bad[np.argmax(bad == 0)] = 1  # group 0 one row short, group 1 one row over
+        base2 = hip.upload(np.concatenate([np.zeros(offset // 4, np.int32), bad]))
+        assert lib.pw4_gidx_to_perm(base2 + offset, k, g, perm, status, None) == 0
+        assert hip.download(status, (1,), np.int32)[0] != 0
+    finally:
+        hip.free_all()
