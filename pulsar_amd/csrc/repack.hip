@@ -582,14 +582,15 @@ hipError_t launch_repack_gptq(const uint32_t* qweight, const int32_t* perm, uint
     if (perm != nullptr && K <= 65535) {
         // act-order through LDS: the widest block (64 or 32 columns in strided
         // groups, else 16 or 8 adjacent) whose words and permutation fit and
-        // whose blocks cover at least half the CUs, else the narrowest that
+        // whose blocks cover at least 0.8 of the CUs, else the narrowest that
         // fits; past that, 8 columns with the permutation read from global
         // memory.  One workgroup per block up to two blocks per CU, else one
         // persistent workgroup per CU.  Measured on MI355X, kernel only, us:
-        // Llama-3-8B gate 15.0 at 64 columns (20.3-21.0 at 32), q 7.4 at 32
-        // (8.1 at 64), k 4.9 at 8 (6.3 at 32), down 24.1 at 16 (the widest
-        // that fits K = 14336); 70B qkv 31.2 with 320 workgroups (37.9 with
-        // 256 walking 1.25 blocks each), gate_up 132 with 256 persistent
+        // Llama-3-8B gate 15.0 at 64 columns (224 blocks; 20.3-21.0 at 32), q
+        // 7.06 at 16 (7.43 at 32 on half the CUs, 8.1 at 64), k 4.9 at 8 (6.3
+        // at 32), down 20.4 at 16 (the widest that fits K = 14336); 70B o 21.9
+        // at 32 (24.1 at 16), qkv 31.2 with 320 workgroups (37.9 with 256
+        // walking 1.25 blocks each), gate_up 132 with 256 persistent
         // workgroups (138 with 512).
         constexpr size_t kLdsCap = 152 * 1024;
         auto words_bytes = [&](int w) { return (size_t)(w / 8) * (K + 4) * 4; };
@@ -603,7 +604,7 @@ hipError_t launch_repack_gptq(const uint32_t* qweight, const int32_t* perm, uint
             for (int w : {64, 32, 16, 8}) {
                 if (!fits(w)) continue;
                 nb = w;
-                if (2 * (npad / w) >= cus) break;
+                if (5 * (npad / w) >= 4 * cus) break;
             }
         }
         if (nb == 0 && words_bytes(8) <= kLdsCap) {
