@@ -532,16 +532,23 @@ int prefill256_tile() { return TM; }
 
 // Tail balancing of an unsplit launch of 256-row tiles: the number of
 // trailing N-tile columns to run as 128-row tiles, and the cost in waves of
-// full tiles (a half tile counts 0.55: its dequant is shared by half the
-// MFMAs; a split must save 0.1 wave).
+// full tiles (a split must save 0.1 wave).  128-row tiles run two per CU: a
+// round of up to 2 x CUs of them costs one wave, and a last round of at most
+// one per CU 0.69 (a chunk per 1.1 us alone against 1.6 for a 256-row tile).
+// Before, every CU-sized group of 128-row tiles counted 0.55 of a wave, which
+// priced a lone tail round too low: bf16 qkv at M = 1024 ran all 24 column
+// tiles as 192 lone 128-row workgroups in 73 us.
 int64_t prefill256_tail_cols(int64_t M, int64_t N, int cus, double* waves) {
+    constexpr double kSoloRound = 1.1 / 1.6;
     const int64_t num_m = ceil_div(M, TM), num_n = ceil_div(N, TN);
     double best = cus > 0 ? (double)ceil_div(num_m * num_n, cus) : 1.0;
     int64_t nt = 0;
     if (cus > 0) {
         for (int64_t t = 1; t <= num_n; ++t) {
-            const double cost = (double)ceil_div(num_m * (num_n - t), cus) +
-                                0.55 * (double)ceil_div(ceil_div(M, TM / 2) * t, cus);
+            const int64_t half = ceil_div(M, TM / 2) * t;  // 128-row tiles of the tail
+            const int64_t pairs = half / (2 * (int64_t)cus), rest = half - pairs * 2 * (int64_t)cus;
+            const double cost = (double)ceil_div(num_m * (num_n - t), cus) + (double)pairs +
+                                (rest == 0 ? 0.0 : rest <= cus ? kSoloRound : 1.0);
             if (cost < best - 0.1) {
                 best = cost;
                 nt = t;

@@ -115,6 +115,22 @@ def test_prefill_splits_70b(lib, layer, m, want):
     assert want in plan(lib, m, k, n), plan(lib, m, k, n)
 
 
+@pytest.mark.parametrize("layer,m,want", [
+    ("qkv", 1024, "rows=128 splits=1 exact=0 khalves=2"), ("o", 1536, "rows=128 splits=1 exact=0 khalves=2"),
+    ("gate_up", 256, "rows=128 splits=1 exact=0 khalves=2"), ("down", 2048, "rows=128 splits=1 exact=0 khalves=2"),
+    ("qkv", 4096, "rows=256 splits=1"), ("gate_up", 4096, "rows=256 splits=1"),
+])
+def test_prefill_bf16_tail_rounds(lib, layer, m, want):
+    """bf16 x (rounded scaling, 256-row tiles allowed).  A 256-row plan whose tail columns would
+    run as 128-row tiles at one per CU is priced at that lone rate (1.1 us a chunk against
+    1.6 for a 256-row tile): the 8B layers below take K halves instead.  Graph periods, us,
+    two runs each, 256-row plan / K halves: qkv M = 1024 83.4, 82.0 / 72.8, 73.8; o M = 1536
+    82.0, 81.8 / 73.1, 73.3; gate_up M = 256 84.5, 83.8 / 75.2, 74.8; down M = 2048 307,
+    299 / 255, 267.  M = 4096 keeps 256-row tiles."""
+    k, n = L8[layer]
+    assert want in plan(lib, m, k, n, DTYPE_BF16), plan(lib, m, k, n, DTYPE_BF16)
+
+
 def test_ct_layout_repacks_past_the_decode_range(lib):
     k, n = L8["o"]
     assert plan(lib, 16, k, n, layout=LAYOUT_CT).startswith("decode")
