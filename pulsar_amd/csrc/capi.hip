@@ -477,7 +477,7 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
         int nb = win ? win_nb : tree ? tree_nb : decode_nb_override();
         if (nb == 0) nb = s > 1 ? 64 : 16;
         while (nb > 16 && ncols % nb != 0) nb /= 2;
-        const int64_t ncg = ceil_div(ncols, nb);
+        int64_t ncg = ceil_div(ncols, nb);
         // ring depth: a unit of at most 4 steps per wave needs no more (its
         // steps pad to the ring depth).  Up to M = 8 the 4-step ring also
         // wins on long units: 8 waves x 4 x 1 KB is 32 KB of weight loads in
@@ -524,15 +524,44 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
             per_cu_max = std::max<int64_t>(std::min<int64_t>(2, (int64_t)(kLdsPerCu / std::max<size_t>(lds_run, 1))), 1);
         }
         per_cu_max = std::min<int64_t>(per_cu_max, 2);
-        int64_t best_wps = 1, best_cost = INT64_MAX;
-        for (int64_t per_cu = 1; per_cu <= per_cu_max; ++per_cu) {
-            const int64_t wps_max = std::max<int64_t>((int64_t)cus * per_cu / s, 1);
-            const int64_t ups = ceil_div(ncg, std::min(wps_max, ncg));
-            const int64_t wps = ceil_div(ncg, ups);
-            const int64_t cost = ups * ceil_div(wps * s, (int64_t)cus);
-            if (cost < best_cost || (cost == best_cost && wps > best_wps)) {
-                best_cost = cost;
-                best_wps = wps;
+        // workgroups per slice for ncg units, and the busiest CU's units
+        auto pick_wps = [&](int64_t units, int64_t* cost_out) {
+            int64_t wps_best = 1, cost_best = INT64_MAX;
+            for (int64_t per_cu = 1; per_cu <= per_cu_max; ++per_cu) {
+                const int64_t wps_max = std::max<int64_t>((int64_t)cus * per_cu / s, 1);
+                const int64_t ups = ceil_div(units, std::min(wps_max, units));
+                const int64_t wps = ceil_div(units, ups);
+                const int64_t cost = ups * ceil_div(wps * s, (int64_t)cus);
+                if (cost < cost_best || (cost == cost_best && wps > wps_best)) {
+                    cost_best = cost;
+                    wps_best = wps;
+                }
+            }
+            if (cost_out) *cost_out = cost_best;
+            return wps_best;
+        };
+        int64_t best_cost = 0;
+        int64_t best_wps = pick_wps(ncg, &best_cost);
+        // One slice over a long K (8192 and up): 32-column units where the
+        // busiest CU gets no more columns than with 16.  Each K wave then
+        // streams twice the steps between unit ends, one workgroup per CU
+        // where 16 columns would take two.  Measured on MI355X (kernel only,
+        // us, 16 / 32 columns): Llama-3-70B o 8192 x 8192 M = 1 9.56 / 8.28,
+        // M = 4 9.28 / 8.84, M = 8 10.32 / 9.72; gate_up 8192 x 57344 M = 1
+        // 45.6 / 40.3, M = 4 43.7 / 40.9, M = 8 46.2 / 41.5.  70B qkv (48
+        // columns on the busiest CU at 16, 64 at 32) and every Llama-3-8B
+        // layer (K = 4096, or more columns per CU at 32) keep 16.
+        // (The ring depth does not change: at K >= 8192 a wave has at least 8
+        // steps per unit either way.)
+        if (!forced && !win && !tree && s == 1 && nb == 16 && decode_nb_override() == 0 && K >= 8192 &&
+            ncols % 32 == 0) {
+            int64_t cost32 = 0;
+            const int64_t wps32 = pick_wps(ceil_div(ncols, 32), &cost32);
+            if (cost32 * 32 <= best_cost * 16) {
+                nb = 32;
+                ncg = ceil_div(ncols, nb);
+                best_wps = wps32;
+                best_cost = cost32;
             }
         }
         if (const char* e = plan_env("PW4_DECODE_WPS")) {  // tuning sweeps only

@@ -29,6 +29,7 @@ LAYOUT_CT, LAYOUT_MARLIN = 0, 1
 G = 128
 L8 = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 28672), "down": (14336, 4096)}
 L70 = {"qkv": (8192, 10240), "gate_up": (8192, 57344), "down": (28672, 8192)}
+L70o = {"o": (8192, 8192)}
 OVERRIDES = ("PW4_PREFILL_ROWS", "PW4_PREFILL_SPLITS", "PW4_PREFILL_KHALVES", "PW4_PREFILL_EXACT",
              "PW4_PREFILL_TILE", "PW4_DECODE", "PW4_DECODE_BLOCK_SCALES", "PW4_DECODE_PERM_LDS", "PW4_DECODE_NB",
              "PW4_DECODE_SPLITS", "PW4_DECODE_WPS", "PW4_DECODE_WIN")
@@ -156,3 +157,27 @@ def test_decode_block_scales_on_large_layers(lib, layer, want, m):
     k, n = (L8 if model == "8b" else L70)[name]
     p = plan(lib, m, k, n)
     assert p.startswith("decode") and f" bs={want}" in p, p
+
+
+@pytest.mark.parametrize("layer,m,want", [
+    ("o", 1, 32), ("o", 4, 32), ("o", 8, 32), ("gate_up", 1, 32), ("gate_up", 8, 32), ("down", 1, 32),
+    ("qkv", 1, 16), ("qkv", 8, 16),
+])
+@pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_BF16])
+def test_decode_unit_width_70b(lib, layer, m, want, dtype):
+    """One slice over K >= 8192: 32-column units where the busiest CU gets no more columns than
+    with 16 (one workgroup per CU, twice the steps per K wave between unit ends).  Kernel only,
+    us, 16 / 32 columns, fp16: 70B o M = 1 9.44 / 8.70, M = 8 10.28 / 9.76; gate_up M = 2
+    44.96 / 39.88, M = 8 45.27 / 40.96; down M = 1 24.48 / 23.66.  70B qkv keeps 16 (48
+    columns on the busiest CU against 64 at 32)."""
+    k, n = L70o[layer] if layer == "o" else L70[layer]
+    p = plan(lib, m, k, n, dtype)
+    assert p.startswith("decode") and f"nb={want} " in p, p
+
+
+@pytest.mark.parametrize("layer", list(L8))
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_decode_unit_width_8b_stays_16(lib, layer, m):
+    k, n = L8[layer]
+    p = plan(lib, m, k, n)
+    assert p.startswith("decode") and ("nb=16 " in p or " tree=1" in p), p
