@@ -446,10 +446,18 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
                 const int nb_forced = decode_nb_override();
                 const bool one_wg_per_cu = 2 * lds_for(p2) > kLdsPerCu;
                 const int64_t busiest16 = ceil_div(ceil_div(ncols, 16) * p2, (int64_t)cus) * 16;
+                // 64-column units also where their slices split evenly over the
+                // CUs and each of a unit's two K waves streams 24 steps or more:
+                // 70B down (K = 28672) at M = 4 / 8, 32 / 64 columns, kernel only,
+                // 24.4 / 22.6 and 27.9 / 24.7 us.  With shorter units 32 columns
+                // stay faster (70B o at M = 16, 16 steps per wave at 64: 12.4 us
+                // at 32).
+                const bool long_units64 = ceil_div(ceil_div(kps_for(p2), 128), 2) >= 24;
                 for (int w : {64, 32, 16}) {
                     const bool fits = M * w <= 1024 && ncols % w == 0;
                     const int64_t q = ceil_div(ncols, w) * p2;  // unit slices
                     const bool wide = q >= (w == 64 ? 3 : 2) * cus ||
+                                      (w == 64 && q % cus == 0 && long_units64) ||
                                       (w == 32 && one_wg_per_cu && ceil_div(q, (int64_t)cus) * 32 <= busiest16);
                     if (nb_forced ? (w == nb_forced && fits) || w == 16 : (fits && wide) || w == 16) {
                         tree_nb = w;

@@ -181,3 +181,16 @@ def test_decode_unit_width_8b_stays_16(lib, layer, m):
     k, n = L8[layer]
     p = plan(lib, m, k, n)
     assert p.startswith("decode") and ("nb=16 " in p or " tree=1" in p), p
+
+
+@pytest.mark.parametrize("layer,k,n,m,want", [
+    ("70b_down", 28672, 8192, 4, 64), ("70b_down", 28672, 8192, 8, 64), ("70b_o", 8192, 8192, 16, 32),
+    ("8b_down", 14336, 4096, 16, 32), ("8b_down", 14336, 4096, 8, 32),
+])
+def test_decode_tree_units_64_on_long_slices(lib, layer, k, n, m, want):
+    """Exchange-tree plans take 64-column units where their slices split evenly over the CUs
+    and each K wave of a unit streams 24 steps or more (70B down, K = 28672, M = 4 / 8:
+    kernel only, 32 / 64 columns, 24.3 / 22.7 and 28.1 / 25.6 us, fp16).  Shorter units keep
+    32 columns (70B o at M = 16, 8B down at M = 8-16)."""
+    p = plan(lib, m, k, n)
+    assert " tree=1" in p and f"nb={want} " in p, p
