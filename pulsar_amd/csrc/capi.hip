@@ -572,6 +572,30 @@ Plan make_plan(int layout, int x_dtype, int stype, bool zp, int64_t M, int64_t N
                 best_cost = cost32;
             }
         }
+        // One slice over a short K (below 8192) at M <= 8: 16-column units give
+        // each K wave only K / 1024 steps per unit (4 at K = 4096).  The widest
+        // of 64 and 32 columns with at most 16 steps per K wave, whose
+        // workgroups cover at least 3/4 of the CUs and whose busiest CU gets at
+        // most 1.15x the columns it would at 16.  Measured on MI355X (kernel
+        // only, us, 16 columns / wider): Llama-3-8B qkv 4096 x 6144 at 32
+        // columns M = 1 5.64 / 5.28, M = 4 6.40 / 5.66, M = 8 6.52 / 6.28;
+        // gate_up 4096 x 28672 at 64 columns M = 1 13.28 / 12.36, M = 4 13.60 /
+        // 12.76, M = 8 14.28 / 14.12.  o (32 columns would leave half the CUs
+        // idle) and down (K = 14336) keep 16; at M = 12 the wider units were
+        // no faster.
+        if (!forced && !win && !tree && s == 1 && nb == 16 && decode_nb_override() == 0 && K < 8192 && M <= 8) {
+            for (int w : {64, 32}) {
+                if (ncols % w != 0 || ceil_div(kps, 128) * w > 16 * 128) continue;
+                int64_t cost_w = 0;
+                const int64_t wps_w = pick_wps(ceil_div(ncols, w), &cost_w);
+                if (4 * wps_w < 3 * (int64_t)cus || 20 * cost_w * w > 23 * best_cost * 16) continue;
+                nb = w;
+                ncg = ceil_div(ncols, nb);
+                best_wps = wps_w;
+                best_cost = cost_w;
+                break;
+            }
+        }
         if (const char* e = plan_env("PW4_DECODE_WPS")) {  // tuning sweeps only
             const int64_t v = std::atoll(e);
             if (v >= 1 && v <= 4 * (int64_t)cus) best_wps = std::min<int64_t>(v, ncg);

@@ -175,12 +175,17 @@ def test_decode_unit_width_70b(lib, layer, m, want, dtype):
     assert p.startswith("decode") and f"nb={want} " in p, p
 
 
-@pytest.mark.parametrize("layer", list(L8))
+@pytest.mark.parametrize("layer,want", [("qkv", 32), ("gate_up", 64), ("o", 16), ("down", 16)])
 @pytest.mark.parametrize("m", [1, 4, 8])
-def test_decode_unit_width_8b_stays_16(lib, layer, m):
+def test_decode_unit_width_8b(lib, layer, want, m):
+    """One slice over K = 4096 at M <= 8: the widest units (at most 16 steps per K wave) whose
+    workgroups cover 3/4 of the CUs with at most 1.15x the busiest CU's columns.  Kernel only,
+    us, 16 columns / wider: qkv at 32 M = 1 5.64 / 5.28, M = 4 6.40 / 5.66, M = 8 6.52 / 6.28;
+    gate_up at 64 M = 1 13.28 / 12.36, M = 4 13.60 / 12.76.  o keeps 16 (32 columns would
+    leave half the CUs idle), and so does down (K = 14336; at M = 8 on the exchange tree)."""
     k, n = L8[layer]
     p = plan(lib, m, k, n)
-    assert p.startswith("decode") and ("nb=16 " in p or " tree=1" in p), p
+    assert p.startswith("decode") and (f"nb={want} " in p or (layer == "down" and " tree=1" in p)), p
 
 
 @pytest.mark.parametrize("layer,k,n,m,want", [

@@ -97,8 +97,10 @@ def test_fused_stack_equals_unfused(m):
     # o and down are the same linear in both stacks: same plan, same bits
     torch.testing.assert_close(yb[1], ya[3], rtol=0, atol=0)
     torch.testing.assert_close(yb[3], ya[6], rtol=0, atol=0)
-    if m == 1:  # one K slice, 16-column units for every shape: identical plans
-        torch.testing.assert_close(yb[0], torch.cat(ya[0:3], dim=1), rtol=0, atol=0)
+    if m == 1:
+        # one K slice, and gate|up takes the 64-column units that gate and up take alone:
+        # identical plans, the same bits (q|k|v takes 32-column units where q, k and v
+        # take 16: a different fp32 summation order, held to one ulp above)
         torch.testing.assert_close(yb[2], torch.cat(ya[4:6], dim=1), rtol=0, atol=0)
 
 
